@@ -1,0 +1,87 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// MFMA operand layouts used throughout (measured on gfx950, wave64):
+//   v_mfma_f32_16x16x32_bf16: A lane l holds A[l%16][8*(l/16) .. +8],
+//     B lane l holds B[8*(l/16) .. +8][l%16], D lane l holds
+//     D[4*(l/16) + r][l%16], r = 0..3.
+//   v_mfma_f32_32x32x16_bf16: A lane l holds A[l%32][8*(l/32) .. +8],
+//     B lane l holds B[8*(l/32) .. +8][l%32], D lane l holds
+//     D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
+//   v_mfma_f32_16x16x4_f32: A lane l holds A[l%16][l/16], B lane l holds
+//     B[l/16][l%16], D as for 16x16x32.
+//   ds_read_b64_tr_b16 (per 16-lane group, lane m supplies address a_m of
+//     four consecutive b16 values): result lane i, element e =
+//     mem[a_{4e + i/4} + (i%4)].
+// Because the reduction index of an MFMA may be permuted freely (as long as
+// A and B agree), kernels choose k-orderings that make every global or LDS
+// access a contiguous 8- or 16-byte vector.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q36 {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int kHq = 16;        // query heads (full attention)
+constexpr int kHkv = 2;        // KV heads
+constexpr int kGroup = kHq / kHkv;
+constexpr int kD = 256;        // head dim
+constexpr int kQDim = kHq * kD;     // 4096
+constexpr int kKvRow = kHkv * kD;   // 512 elements per cache row
+constexpr int kRotary = 64;
+constexpr int kRotaryPairs = kRotary / 2;
+constexpr float kRopeTheta = 1.0e7f;
+constexpr unsigned kMaxTokens = 262144u;
+
+// Gated DeltaNet geometry.
+constexpr int kGdnHk = 16, kGdnHv = 32, kGdnDk = 128, kGdnDv = 128;
+constexpr int kGdnConvDim = 2 * kGdnHk * kGdnDk + kGdnHv * kGdnDv;  // 8192
+constexpr int kGdnConvK = 4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
+__device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }  // RNE
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Transposed LDS read of four b16 values (see layout note above).
+__device__ __forceinline__ i16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+__device__ __forceinline__ bf16x8 cat_bf16x8(i16x4 lo, i16x4 hi) {
+  i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+
+}  // namespace q36
+
+#define Q36_EXPORT extern "C" __attribute__((visibility("default")))
+
+// hipError_t values returned through the C ABI (the reference's providers
+// return a hipError_t as int, qrt_ck_fmha_q8192_provider.cpp:141-146).
+#define Q36_OK 0
+#define Q36_EINVAL 1  // hipErrorInvalidValue

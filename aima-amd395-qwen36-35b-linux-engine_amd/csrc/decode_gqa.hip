@@ -1,0 +1,333 @@
+// Split-K GQA flash-decode over a resident sequence-major BF16 KV cache.
+//
+// Replaces the reference's decode core launch_native_grouped_full_attention
+// (native/src/native_full_attention.hip.cpp:681-765): write the new K/V row,
+// then softmax(q K^T / 16) V for 16 query heads over 2 KV heads (head h reads
+// KV head h/8), D = 256, cache rows [0, cache_end).  The reference streams
+// the whole cache through hipBLASLt QK, 1-5 softmax kernels over bf16 scores
+// and a hipBLASLt PV; here one pass streams K and V exactly once.
+//
+// Layout: k_cache, v_cache are [capacity, 2, 256] bf16 (token stride 512).
+//
+// Kernel plan (HBM-bound, 2048 bytes of K+V per token):
+//  * grid = (nsplit, 2 KV heads); a workgroup owns a contiguous token range
+//    of one KV head; its 4 waves take 32-token blocks round-robin.
+//  * per block: S^T = K Q^T on MFMA 16x16x32 (A = K streamed from HBM into
+//    registers, B = the 8 query heads of the group, padded to 16 columns),
+//    online softmax per head in fp32 (exp2 domain), then O^T += V^T P^T on
+//    MFMA with V staged row-major in LDS and read transposed with
+//    ds_read_b64_tr_b16.  The P^T operand is the S^T accumulator itself
+//    (same lane mapping), so no shuffles are needed between the two MFMAs.
+//  * the 4 waves merge in LDS; the workgroup writes one (m, l, O) partial.
+//  * decode_gqa_combine merges the partials of all splits, normalises,
+//    optionally applies the sigmoid output gate, and writes bf16.
+#include "common.h"
+
+namespace q36 {
+namespace {
+
+constexpr int kDecWaves = 4;
+constexpr int kDecBlock = 32;          // tokens per wave iteration
+constexpr int kVPitch = 544;           // LDS row pitch in bytes (512 + 32)
+constexpr int kDecLds = kDecWaves * kDecBlock * kVPitch;  // 69632 bytes
+
+__global__ void write_kv_row_kernel(const bf16* __restrict__ k_new,
+                                    const bf16* __restrict__ v_new,
+                                    bf16* __restrict__ k_cache,
+                                    bf16* __restrict__ v_cache,
+                                    unsigned position) {
+  const unsigned i = threadIdx.x;  // 64 threads x 8 elements = 512
+  const size_t base = (size_t)position * kKvRow;
+  const uint4 kv = reinterpret_cast<const uint4*>(k_new)[i];
+  const uint4 vv = reinterpret_cast<const uint4*>(v_new)[i];
+  reinterpret_cast<uint4*>(k_cache + base)[i] = kv;
+  reinterpret_cast<uint4*>(v_cache + base)[i] = vv;
+}
+
+__global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k_cache,
+    const bf16* __restrict__ v_cache, unsigned cache_end,
+    unsigned split_tokens, unsigned nsplit, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
+  __shared__ __attribute__((aligned(16))) char lds[kDecLds];
+  const int kvh = blockIdx.y;
+  const unsigned split = blockIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;   // MFMA row/column index
+  const int lg = lane >> 4;   // 16-lane group
+  const unsigned begin = split * split_tokens;
+  const unsigned end = min(begin + split_tokens, cache_end);
+
+  // B operand Q^T: column li = query head (kvh*8 + li) for li < 8, zero
+  // padding otherwise.  Reduction slot (lg, s, e) <-> dim lg*64 + s*8 + e, so
+  // each lane reads one contiguous 128-byte run of q and of every K row.
+  bf16x8 qf[8];
+  if (li < kGroup) {
+    const bf16x8* qp = reinterpret_cast<const bf16x8*>(
+        q + (size_t)(kvh * kGroup + li) * kD + lg * 64);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = qp[s];
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
+  }
+
+  f32x4 o[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+  const float scale = 0.0625f * kLog2e;
+  char* vbuf = lds + wave * kDecBlock * kVPitch;
+
+  for (unsigned t0 = begin + wave * kDecBlock; t0 < end;
+       t0 += kDecWaves * kDecBlock) {
+    // K fragments for two 16-token tiles (A operand rows = tokens).
+    bf16x8 kf[2][8];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const unsigned tok = t0 + tt * 16 + li;
+      if (tok < end) {
+        const bf16x8* kp = reinterpret_cast<const bf16x8*>(
+            k_cache + ((size_t)tok * kHkv + kvh) * kD + lg * 64);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kf[tt][s] = kp[s];
+      } else {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) kf[tt][s] = bf16x8{};
+      }
+    }
+    // V rows into registers: row = 2c + lane/32, 16-byte chunk = lane%32.
+    uint4 vr[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const unsigned tok = t0 + 2 * c + (lane >> 5);
+      if (tok < end) {
+        vr[c] = *reinterpret_cast<const uint4*>(
+            v_cache + ((size_t)tok * kHkv + kvh) * kD + (lane & 31) * 8);
+      } else {
+        vr[c] = uint4{0u, 0u, 0u, 0u};
+      }
+    }
+
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      s0 = mfma16x16x32(kf[0][s], qf[s], s0);
+      s1 = mfma16x16x32(kf[1][s], qf[s], s1);
+    }
+    // Lane holds S^T[token t0 + 16*tt + 4*lg + r][head li].
+    float sc[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const unsigned ta = t0 + 4 * lg + r;
+      sc[r] = ta < end ? s0[r] * scale : -INFINITY;
+      sc[4 + r] = ta + 16 < end ? s1[r] * scale : -INFINITY;
+    }
+    float mx = sc[0];
+#pragma unroll
+    for (int r = 1; r < 8; ++r) mx = fmaxf(mx, sc[r]);
+    mx = wave_max_xor(mx, 16);
+    mx = wave_max_xor(mx, 32);
+    const float mnew = fmaxf(m, mx);
+    const float alpha = exp2f(m - mnew);
+    float p[8];
+    float psum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      p[r] = exp2f(sc[r] - mnew);
+      psum += p[r];
+    }
+    l = l * alpha + psum;
+    m = mnew;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[i] *= alpha;
+
+    // Stage V (row-major, padded pitch) in this wave's private LDS slot.
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      *reinterpret_cast<uint4*>(vbuf + (2 * c + (lane >> 5)) * kVPitch +
+                                (lane & 31) * 16) = vr[c];
+    }
+    bf16x8 pb;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) pb[r] = f2bf(p[r]);
+    // O^T[d][head] += V^T[d][tok] P^T[tok][head]; reduction slots (lg, e)
+    // map to tokens 4*lg + e (e < 4) and 16 + 4*lg + (e-4) (e >= 4).
+    const char* row_a = vbuf + (4 * lg + (li >> 2)) * kVPitch + (li & 3) * 8;
+    const char* row_b = row_a + 16 * kVPitch;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt) {
+      const i16x4 a0 = lds_read_tr16(row_a + dt * 32);
+      const i16x4 a1 = lds_read_tr16(row_b + dt * 32);
+      o[dt] = mfma16x16x32(cat_bf16x8(a0, a1), pb, o[dt]);
+    }
+  }
+  // Row sums are split over the 4 lane groups; max is already uniform.
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+
+  // Merge the 4 waves: O^T lane (head li, dims dt*16 + 4*lg + r).
+  __syncthreads();
+  float* mo = reinterpret_cast<float*>(lds);          // [4][8][256]
+  float* mml = mo + kDecWaves * kGroup * kD;           // [4][8][2]
+  if (li < kGroup) {
+    float* dst = mo + (wave * kGroup + li) * kD + 4 * lg;
+#pragma unroll
+    for (int dt = 0; dt < 16; ++dt)
+      *reinterpret_cast<f32x4*>(dst + dt * 16) = o[dt];
+    if (lg == 0) {
+      mml[(wave * kGroup + li) * 2 + 0] = m;
+      mml[(wave * kGroup + li) * 2 + 1] = l;
+    }
+  }
+  __syncthreads();
+  {
+    const int h = threadIdx.x >> 5;          // 0..7
+    const int d0 = (threadIdx.x & 31) * 8;   // 8 dims per thread
+    float mw[kDecWaves], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      mw[w] = mml[(w * kGroup + h) * 2];
+      M = fmaxf(M, mw[w]);
+    }
+    float L = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      const float f = (mw[w] == -INFINITY) ? 0.f : exp2f(mw[w] - M);
+      L += f * mml[(w * kGroup + h) * 2 + 1];
+      const float* src = mo + (w * kGroup + h) * kD + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += f * src[e];
+    }
+    const size_t slot = ((size_t)kvh * nsplit + split) * kGroup + h;
+    float* dst = ws_o + slot * kD + d0;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+    if ((threadIdx.x & 31) == 0) {
+      ws_ml[slot * 2] = M;
+      ws_ml[slot * 2 + 1] = L;
+    }
+  }
+}
+
+// grid = (16 heads, 8 chunks of 32 dims); block = 256 = 32 dims x 8 lanes of
+// splits.
+__global__ __launch_bounds__(256) void decode_gqa_combine_kernel(
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+    unsigned nsplit, const bf16* __restrict__ gate, unsigned gate_head_stride,
+    bf16* __restrict__ out) {
+  __shared__ float red[256];
+  __shared__ float part_acc[8][32];
+  __shared__ float part_l[8];
+  const int head = blockIdx.x;
+  const int kvh = head / kGroup, hh = head % kGroup;
+  const int dsub = threadIdx.x & 31, sg = threadIdx.x >> 5;
+  const int d = blockIdx.y * 32 + dsub;
+  const size_t base = (size_t)kvh * nsplit * kGroup + hh;  // slot of split 0
+
+  float M = -INFINITY;
+  for (unsigned s = threadIdx.x; s < nsplit; s += 256)
+    M = fmaxf(M, ws_ml[(base + (size_t)s * kGroup) * 2]);
+  red[threadIdx.x] = M;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w)
+      red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
+    __syncthreads();
+  }
+  M = red[0];
+  float acc = 0.f, lsum = 0.f;
+  for (unsigned s = sg; s < nsplit; s += 8) {
+    const size_t slot = base + (size_t)s * kGroup;
+    const float ms = ws_ml[slot * 2];
+    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    acc += f * ws_o[slot * kD + d];
+    lsum += f * ws_ml[slot * 2 + 1];
+  }
+  part_acc[sg][dsub] = acc;
+  if (dsub == 0) part_l[sg] = lsum;
+  __syncthreads();
+  if (sg == 0) {
+    float a = 0.f, L = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      a += part_acc[i][dsub];
+      L += part_l[i];
+    }
+    float v = a / L;
+    bf16 ob = f2bf(v);
+    if (gate != nullptr) {
+      // Reference gate numerics (native_pointwise.hip.cpp:207-222): sigmoid in
+      // fp32, rounded to bf16, product rounded to bf16.
+      const float gv = bf2f(gate[(size_t)head * gate_head_stride + d]);
+      const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv)));
+      ob = f2bf(bf2f(ob) * bf2f(sg_b));
+    }
+    out[head * kD + d] = ob;
+  }
+}
+
+unsigned choose_split_tokens(unsigned cache_end) {
+  // Aim for ~2 workgroups per CU-slot (256 CUs) on both KV heads while
+  // keeping at least one 32-token block per wave.
+  const unsigned target_splits = 256;
+  unsigned per = (cache_end + target_splits - 1) / target_splits;
+  const unsigned quantum = kDecWaves * kDecBlock;  // 128
+  per = (per + quantum - 1) / quantum * quantum;
+  if (per < quantum) per = quantum;
+  return per;
+}
+
+}  // namespace
+}  // namespace q36
+
+using namespace q36;
+
+Q36_EXPORT size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
+                                                    unsigned split_tokens) {
+  if (cache_end == 0) return 0;
+  const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
+  const size_t nsplit = (cache_end + per - 1) / per;
+  return nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
+}
+
+Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
+                                 const void* v_new, void* k_cache,
+                                 void* v_cache, unsigned position,
+                                 unsigned cache_end, unsigned capacity,
+                                 const void* gate, unsigned gate_head_stride,
+                                 void* out, void* workspace,
+                                 size_t workspace_bytes, unsigned split_tokens,
+                                 void* stream) {
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
+      out == nullptr || workspace == nullptr || cache_end == 0 ||
+      cache_end > capacity || capacity > kMaxTokens ||
+      ((k_new == nullptr) != (v_new == nullptr)) ||
+      (k_new != nullptr && position >= cache_end) ||
+      (split_tokens % (kDecWaves * kDecBlock)) != 0)
+    return Q36_EINVAL;
+  const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
+  const unsigned nsplit = (cache_end + per - 1) / per;
+  const size_t need = (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
+  if (workspace_bytes < need) return Q36_EINVAL;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (k_new != nullptr) {
+    hipLaunchKernelGGL(write_kv_row_kernel, dim3(1), dim3(64), 0, st,
+                       static_cast<const bf16*>(k_new),
+                       static_cast<const bf16*>(v_new),
+                       static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
+                       position);
+  }
+  float* ws_o = static_cast<float*>(workspace);
+  float* ws_ml = ws_o + (size_t)nsplit * kHkv * kGroup * kD;
+  hipLaunchKernelGGL(decode_gqa_split_kernel, dim3(nsplit, kHkv), dim3(256), 0,
+                     st, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k_cache),
+                     static_cast<const bf16*>(v_cache), cache_end, per, nsplit,
+                     ws_o, ws_ml);
+  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / 32), dim3(256),
+                     0, st, ws_o, ws_ml, nsplit, static_cast<const bf16*>(gate),
+                     gate_head_stride, static_cast<bf16*>(out));
+  return static_cast<int>(hipGetLastError());
+}

@@ -1,0 +1,205 @@
+// Pointwise pieces of the gated full-attention layer.
+//
+//  * qwen36_rotary_table      -- fp32 cos/sin of (position * inv_freq[i]),
+//    i < 32 (native_pointwise.hip.cpp:224-238; four_layer_mini_engine.py
+//    :4470-4471, :4489-4498).
+//  * qwen36_head_norm_rope    -- per-head RMSNorm with the (w + 1) weight,
+//    then rotate-half RoPE on dims [0, 64), for the 16 query heads and the 2
+//    key heads; K and the raw V are written straight into the cache rows
+//    [position_start, position_start + T) (native_pointwise.hip.cpp:242-337,
+//    four_layer_mini_engine.py:5151-5162, :5980-5986).
+//  * qwen36_output_gate       -- attn * sigmoid(gate) with the gate read from
+//    the fused [Q | Gate] q-projection rows (native_pointwise.hip.cpp:207-222
+//    for bf16 attention, :339-359 for fp32 attention; fle:6650).
+//
+// Rounding points follow the eager PyTorch text: every fp32 product and sum
+// that the reference materialises is rounded separately (no contraction).
+#include "common.h"
+
+namespace q36 {
+namespace {
+
+// 1 / 1e7^(2i/64), i = 0..31, each correctly rounded to fp32.
+__constant__ float c_inv_freq[kRotaryPairs];
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
+
+// Correctly rounded fp32 reciprocal square root via fp64.
+__device__ __forceinline__ float rsqrt_rn(float x) {
+  return (float)(1.0 / sqrt((double)x));
+}
+
+__global__ void rotary_table_kernel(float* __restrict__ cosv,
+                                    float* __restrict__ sinv, unsigned tokens,
+                                    unsigned position_start) {
+  const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tokens * kRotaryPairs) return;
+  const unsigned t = i / kRotaryPairs, pair = i % kRotaryPairs;
+  const float angle = mul_rn((float)(position_start + t), c_inv_freq[pair]);
+  cosv[i] = cosf(angle);
+  sinv[i] = sinf(angle);
+}
+
+// grid = (T, 18): y < 16 -> query head y, else key head y - 16.  block = 64;
+// lane holds dims 4*lane .. 4*lane+3 (lanes 0-7: [0,32), lanes 8-15: [32,64)).
+__global__ __launch_bounds__(64) void head_norm_rope_kernel(
+    const bf16* __restrict__ q_gate, unsigned q_row_stride,
+    const bf16* __restrict__ k_raw, unsigned k_row_stride,
+    const bf16* __restrict__ v_raw, unsigned v_row_stride,
+    const bf16* __restrict__ q_weight, const bf16* __restrict__ k_weight,
+    unsigned position_start, bf16* __restrict__ q_out,
+    bf16* __restrict__ k_cache, bf16* __restrict__ v_cache) {
+  const unsigned t = blockIdx.x;
+  const int hsel = blockIdx.y;
+  const bool is_q = hsel < kHq;
+  const int head = is_q ? hsel : hsel - kHq;
+  const int lane = threadIdx.x;
+  const bf16* src = is_q ? q_gate + (size_t)t * q_row_stride + head * 2 * kD
+                         : k_raw + (size_t)t * k_row_stride + head * kD;
+  const bf16* w = is_q ? q_weight : k_weight;
+
+  float x[4], sq[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = bf2f(src[4 * lane + e]);
+    sq[e] = mul_rn(x[e], x[e]);
+  }
+  float sum = add_rn(add_rn(sq[0], sq[1]), add_rn(sq[2], sq[3]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum = add_rn(sum, __shfl_xor(sum, o, 64));
+  const float var = mul_rn(sum, 1.0f / 256.0f);
+  const float inv = rsqrt_rn(add_rn(var, 1e-6f));
+
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float wp1 = add_rn(bf2f(w[4 * lane + e]), 1.0f);
+    y[e] = bf2f(f2bf(mul_rn(mul_rn(x[e], inv), wp1)));
+  }
+  // RoPE on dims [0, 64): lane < 8 pairs with lane + 8.
+  float mate[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) mate[e] = __shfl_xor(y[e], 8, 64);
+  if (lane < 16) {
+    const float pos = (float)(position_start + t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int pair = (4 * lane + e) & (kRotaryPairs - 1);
+      const float angle = mul_rn(pos, c_inv_freq[pair]);
+      const float c = cosf(angle), s = sinf(angle);
+      y[e] = lane < 8 ? sub_rn(mul_rn(y[e], c), mul_rn(mate[e], s))
+                      : add_rn(mul_rn(y[e], c), mul_rn(mate[e], s));
+    }
+  }
+  const size_t pos = position_start + t;
+  bf16* dst = is_q ? q_out + ((size_t)t * kHq + head) * kD
+                   : k_cache + (pos * kHkv + head) * kD;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[4 * lane + e] = f2bf(y[e]);
+  if (!is_q) {
+    const bf16* vs = v_raw + (size_t)t * v_row_stride + head * kD;
+    bf16* vd = v_cache + (pos * kHkv + head) * kD;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) vd[4 * lane + e] = vs[4 * lane + e];
+  }
+}
+
+template <bool kF32>
+__global__ void output_gate_kernel(const void* __restrict__ attn,
+                                   const bf16* __restrict__ q_gate,
+                                   unsigned q_row_stride, bf16* __restrict__ out,
+                                   unsigned tokens) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)tokens * kQDim) return;
+  const size_t t = i / kQDim;
+  const int f = (int)(i - t * kQDim);
+  const int head = f / kD, d = f % kD;
+  const bf16 a = kF32 ? f2bf(static_cast<const float*>(attn)[i])
+                      : static_cast<const bf16*>(attn)[i];
+  const float gv = bf2f(q_gate[t * q_row_stride + head * 2 * kD + kD + d]);
+  const bf16 sg = f2bf(1.0f / (1.0f + expf(-gv)));
+  out[i] = f2bf(mul_rn(bf2f(a), bf2f(sg)));
+}
+
+bool g_freq_ready[64] = {};
+
+int ensure_inv_freq() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return Q36_EINVAL;
+  if (g_freq_ready[dev]) return Q36_OK;
+  float h[kRotaryPairs];
+  for (int i = 0; i < kRotaryPairs; ++i)
+    h[i] = (float)(1.0 / pow(1.0e7, (2.0 * i) / (double)kRotary));
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(c_inv_freq), h, sizeof(h));
+  if (e != hipSuccess) return (int)e;
+  g_freq_ready[dev] = true;
+  return Q36_OK;
+}
+
+}  // namespace
+}  // namespace q36
+
+using namespace q36;
+
+Q36_EXPORT int qwen36_rotary_table(float* cosv, float* sinv, unsigned tokens,
+                                   unsigned position_start, void* stream) {
+  if (cosv == nullptr || sinv == nullptr || tokens == 0 ||
+      (size_t)position_start + tokens > kMaxTokens)
+    return Q36_EINVAL;
+  const int st = ensure_inv_freq();
+  if (st != Q36_OK) return st;
+  const unsigned n = tokens * kRotaryPairs;
+  hipLaunchKernelGGL(rotary_table_kernel, dim3((n + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), cosv, sinv, tokens,
+                     position_start);
+  return static_cast<int>(hipGetLastError());
+}
+
+Q36_EXPORT int qwen36_head_norm_rope(
+    const void* q_gate, unsigned q_row_stride, const void* k_raw,
+    unsigned k_row_stride, const void* v_raw, unsigned v_row_stride,
+    const void* q_weight, const void* k_weight, unsigned tokens,
+    unsigned position_start, void* q_out, void* k_cache, void* v_cache,
+    void* stream) {
+  if (q_gate == nullptr || k_raw == nullptr || v_raw == nullptr ||
+      q_weight == nullptr || k_weight == nullptr || q_out == nullptr ||
+      k_cache == nullptr || v_cache == nullptr || tokens == 0 ||
+      (size_t)position_start + tokens > kMaxTokens ||
+      q_row_stride < 2 * kQDim || k_row_stride < kKvRow ||
+      v_row_stride < kKvRow)
+    return Q36_EINVAL;
+  const int st = ensure_inv_freq();
+  if (st != Q36_OK) return st;
+  hipLaunchKernelGGL(head_norm_rope_kernel, dim3(tokens, kHq + kHkv), dim3(64),
+                     0, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16*>(q_gate), q_row_stride,
+                     static_cast<const bf16*>(k_raw), k_row_stride,
+                     static_cast<const bf16*>(v_raw), v_row_stride,
+                     static_cast<const bf16*>(q_weight),
+                     static_cast<const bf16*>(k_weight), position_start,
+                     static_cast<bf16*>(q_out), static_cast<bf16*>(k_cache),
+                     static_cast<bf16*>(v_cache));
+  return static_cast<int>(hipGetLastError());
+}
+
+Q36_EXPORT int qwen36_output_gate(const void* attn, int attn_is_f32,
+                                  const void* q_gate, unsigned q_row_stride,
+                                  void* out, unsigned tokens, void* stream) {
+  if (attn == nullptr || q_gate == nullptr || out == nullptr || tokens == 0 ||
+      q_row_stride < 2 * kQDim)
+    return Q36_EINVAL;
+  const size_t n = (size_t)tokens * kQDim;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (attn_is_f32)
+    hipLaunchKernelGGL(output_gate_kernel<true>, grid, dim3(256), 0, st, attn,
+                       static_cast<const bf16*>(q_gate), q_row_stride,
+                       static_cast<bf16*>(out), tokens);
+  else
+    hipLaunchKernelGGL(output_gate_kernel<false>, grid, dim3(256), 0, st, attn,
+                       static_cast<const bf16*>(q_gate), q_row_stride,
+                       static_cast<bf16*>(out), tokens);
+  return static_cast<int>(hipGetLastError());
+}

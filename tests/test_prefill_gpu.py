@@ -1,0 +1,82 @@
+"""GPU parity of the causal GQA FMHA prefill (provider ABI) against the CPU
+oracle (four_layer_mini_engine.py:6627-6648 SDPA, fp32 evaluation)."""
+import pytest
+import torch
+
+from oracle import attention_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2        # max-abs-err bar (north_star)
+TOL_TIGHT = 5e-3  # fp32 output vs fp32 oracle: only P's bf16 rounding differs
+
+
+def _inputs(t, s, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(t, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("t,s", [(1, 1), (7, 7), (64, 64), (128, 128), (300, 300),
+                                 (1, 513), (100, 4196), (129, 257), (1000, 1000),
+                                 (512, 2048)])
+def test_prefill_matches_oracle(gpu, t, s):
+    from qwen36_attn.full_attention import fmha_prefill
+    q, k, v = _inputs(t, s, seed=t * 7 + s)
+    print(f"prefill T={t} S={s}", flush=True)
+    got = fmha_prefill(q.to(gpu), k.to(gpu), v.to(gpu)).cpu()
+    ref = O.prefill_attention(q, k, v, position_start=s - t, out_dtype=torch.float32)
+    err = (got - ref).abs().max().item()
+    assert torch.isfinite(got).all()
+    assert err <= TOL_TIGHT, err
+
+
+def test_prefill_config3_sampled_rows(gpu):
+    """Config 3: 8192 new tokens over a 4096-token cached prefix (S=12288).
+    Rows are independent, so a spread of rows (first, last, tile edges) is
+    checked exactly against the oracle restricted to those rows."""
+    from qwen36_attn.full_attention import fmha_prefill
+    t, s = 8192, 12288
+    q, k, v = _inputs(t, s, seed=3)
+    print("prefill config3", flush=True)
+    got = fmha_prefill(q.to(gpu), k.to(gpu), v.to(gpu)).cpu()
+    rows = torch.tensor([0, 1, 63, 64, 127, 128, 129, 2047, 4095, 4096, 6000, 8190, 8191])
+    off = s - t
+    for r in rows.tolist():
+        lim = r + off + 1
+        ref = O.prefill_attention(q[r:r + 1], k[:lim], v[:lim], position_start=lim - 1,
+                                  out_dtype=torch.float32)
+        assert (got[r:r + 1] - ref).abs().max().item() <= TOL_TIGHT, r
+    assert torch.isfinite(got).all()
+
+
+def test_prefix_extension_equals_tail_of_full_prefill(gpu):
+    """Bottom-right prefill over S equals the last T rows of a full causal
+    prefill over S (prefix-cache continuation)."""
+    from qwen36_attn.full_attention import fmha_prefill
+    s, t = 1500, 700
+    q, k, v = _inputs(s, s, seed=21)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    full = fmha_prefill(qd, kd, vd)
+    tail = fmha_prefill(qd[s - t:].contiguous(), kd, vd)
+    torch.cuda.synchronize()
+    assert (full[s - t:] - tail).abs().max().item() <= 1e-6
+
+
+def test_provider_mirror_and_errors(gpu):
+    from qwen36_attn import _lib
+    from qwen36_attn.full_attention import FmhaProvider
+    lib = _lib.load()
+    assert lib.qrt_ck_fmha_prepare(0) == 1
+    assert lib.qrt_ck_fmha_prepare(262145) == 1
+    assert lib.qrt_ck_fmha_prepare(8192) == 0
+    # kv_tokens < query_tokens is rejected without a launch.
+    assert lib.qrt_ck_fmha_bf16_launch_ex(None, None, None, None, 4, 2, None) == 1
+    prov = FmhaProvider()
+    q, k, v = _inputs(256, 256, seed=2)
+    out = prov.launch_ck_fmha(q=q.to(gpu), k=k.to(gpu), value=v.to(gpu))
+    ref = O.prefill_attention(q, k, v, 0, out_dtype=torch.float32)
+    assert (out.cpu() - ref).abs().max().item() <= TOL_TIGHT
+    prov.release()
