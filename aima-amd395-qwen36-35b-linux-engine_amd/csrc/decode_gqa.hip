@@ -31,22 +31,10 @@ constexpr int kDecBlock = 32;          // tokens per wave iteration
 constexpr int kVPitch = 544;           // LDS row pitch in bytes (512 + 32)
 constexpr int kDecLds = kDecWaves * kDecBlock * kVPitch;  // 69632 bytes
 
-__global__ void write_kv_row_kernel(const bf16* __restrict__ k_new,
-                                    const bf16* __restrict__ v_new,
-                                    bf16* __restrict__ k_cache,
-                                    bf16* __restrict__ v_cache,
-                                    unsigned position) {
-  const unsigned i = threadIdx.x;  // 64 threads x 8 elements = 512
-  const size_t base = (size_t)position * kKvRow;
-  const uint4 kv = reinterpret_cast<const uint4*>(k_new)[i];
-  const uint4 vv = reinterpret_cast<const uint4*>(v_new)[i];
-  reinterpret_cast<uint4*>(k_cache + base)[i] = kv;
-  reinterpret_cast<uint4*>(v_cache + base)[i] = vv;
-}
-
 __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k_cache,
-    const bf16* __restrict__ v_cache, unsigned cache_end,
+    const bf16* __restrict__ q, bf16* __restrict__ k_cache,
+    bf16* __restrict__ v_cache, const bf16* __restrict__ k_new,
+    const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
     unsigned split_tokens, unsigned nsplit, float* __restrict__ ws_o,
     float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) char lds[kDecLds];
@@ -58,6 +46,20 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   const int lg = lane >> 4;   // 16-lane group
   const unsigned begin = split * split_tokens;
   const unsigned end = min(begin + split_tokens, cache_end);
+  // The workgroup whose range holds the new row writes it to the cache (this
+  // KV head's half) and reads K/V for that token from k_new/v_new directly,
+  // so no other workgroup depends on the write.
+  const bool has_new = k_new != nullptr && position >= begin && position < end;
+  if (has_new && wave == 0) {
+    const size_t o = ((size_t)position * kHkv + kvh) * kD;
+    if (lane < 32) {
+      reinterpret_cast<uint4*>(k_cache + o)[lane] =
+          reinterpret_cast<const uint4*>(k_new + kvh * kD)[lane];
+    } else {
+      reinterpret_cast<uint4*>(v_cache + o)[lane - 32] =
+          reinterpret_cast<const uint4*>(v_new + kvh * kD)[lane - 32];
+    }
+  }
 
   // B operand Q^T: column li = query head (kvh*8 + li) for li < 8, zero
   // padding otherwise.  Reduction slot (lg, s, e) <-> dim lg*64 + s*8 + e, so
@@ -88,8 +90,10 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     for (int tt = 0; tt < 2; ++tt) {
       const unsigned tok = t0 + tt * 16 + li;
       if (tok < end) {
-        const bf16x8* kp = reinterpret_cast<const bf16x8*>(
-            k_cache + ((size_t)tok * kHkv + kvh) * kD + lg * 64);
+        const bf16* krow = (has_new && tok == position)
+                               ? k_new + kvh * kD
+                               : k_cache + ((size_t)tok * kHkv + kvh) * kD;
+        const bf16x8* kp = reinterpret_cast<const bf16x8*>(krow + lg * 64);
 #pragma unroll
         for (int s = 0; s < 8; ++s) kf[tt][s] = kp[s];
       } else {
@@ -103,8 +107,10 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     for (int c = 0; c < 16; ++c) {
       const unsigned tok = t0 + 2 * c + (lane >> 5);
       if (tok < end) {
-        vr[c] = *reinterpret_cast<const uint4*>(
-            v_cache + ((size_t)tok * kHkv + kvh) * kD + (lane & 31) * 8);
+        const bf16* vrow = (has_new && tok == position)
+                               ? v_new + kvh * kD
+                               : v_cache + ((size_t)tok * kHkv + kvh) * kD;
+        vr[c] = *reinterpret_cast<const uint4*>(vrow + (lane & 31) * 8);
       } else {
         vr[c] = uint4{0u, 0u, 0u, 0u};
       }
@@ -211,52 +217,66 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   }
 }
 
-// grid = (16 heads, 8 chunks of 32 dims); block = 256 = 32 dims x 8 lanes of
-// splits.
-__global__ __launch_bounds__(256) void decode_gqa_combine_kernel(
+// grid = (16 heads, 8 chunks of 32 dims); block = 512 = 32 dims x 16 split
+// groups.  Every thread issues all of its partial loads before using any
+// (up to kCombinePer splits), merges them online in registers, and the 16
+// groups are merged through LDS.
+constexpr int kCombineGroups = 16;
+constexpr int kCombinePer = 16;
+constexpr unsigned kMaxSplits = kCombineGroups * kCombinePer;  // 256
+
+__global__ __launch_bounds__(512) void decode_gqa_combine_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     unsigned nsplit, const bf16* __restrict__ gate, unsigned gate_head_stride,
     bf16* __restrict__ out) {
-  __shared__ float red[256];
-  __shared__ float part_acc[8][32];
-  __shared__ float part_l[8];
+  __shared__ float part_m[kCombineGroups][32];
+  __shared__ float part_a[kCombineGroups][32];
+  __shared__ float part_l[kCombineGroups][32];
   const int head = blockIdx.x;
   const int kvh = head / kGroup, hh = head % kGroup;
   const int dsub = threadIdx.x & 31, sg = threadIdx.x >> 5;
   const int d = blockIdx.y * 32 + dsub;
   const size_t base = (size_t)kvh * nsplit * kGroup + hh;  // slot of split 0
 
+  float ms[kCombinePer], os[kCombinePer], ls[kCombinePer];
+#pragma unroll
+  for (int u = 0; u < kCombinePer; ++u) {
+    const unsigned sp = sg + kCombineGroups * u;
+    const size_t slot = base + (size_t)sp * kGroup;
+    const bool ok = sp < nsplit;
+    ms[u] = ok ? ws_ml[slot * 2] : -INFINITY;
+    ls[u] = ok ? ws_ml[slot * 2 + 1] : 0.f;
+    os[u] = ok ? ws_o[slot * kD + d] : 0.f;
+  }
   float M = -INFINITY;
-  for (unsigned s = threadIdx.x; s < nsplit; s += 256)
-    M = fmaxf(M, ws_ml[(base + (size_t)s * kGroup) * 2]);
-  red[threadIdx.x] = M;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w)
-      red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + w]);
-    __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kCombinePer; ++u) M = fmaxf(M, ms[u]);
+  float acc = 0.f, L = 0.f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int u = 0; u < kCombinePer; ++u) {
+      const float f = exp2f(ms[u] - M);  // 0 for empty splits (ms = -inf)
+      acc += f * os[u];
+      L += f * ls[u];
+    }
   }
-  M = red[0];
-  float acc = 0.f, lsum = 0.f;
-  for (unsigned s = sg; s < nsplit; s += 8) {
-    const size_t slot = base + (size_t)s * kGroup;
-    const float ms = ws_ml[slot * 2];
-    const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
-    acc += f * ws_o[slot * kD + d];
-    lsum += f * ws_ml[slot * 2 + 1];
-  }
-  part_acc[sg][dsub] = acc;
-  if (dsub == 0) part_l[sg] = lsum;
+  part_m[sg][dsub] = M;
+  part_a[sg][dsub] = acc;
+  part_l[sg][dsub] = L;
   __syncthreads();
   if (sg == 0) {
-    float a = 0.f, L = 0.f;
+    float Mg = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      a += part_acc[i][dsub];
-      L += part_l[i];
+    for (int i = 0; i < kCombineGroups; ++i) Mg = fmaxf(Mg, part_m[i][dsub]);
+    float a = 0.f, Lg = 0.f;
+#pragma unroll
+    for (int i = 0; i < kCombineGroups; ++i) {
+      const float mi = part_m[i][dsub];
+      const float f = mi == -INFINITY ? 0.f : exp2f(mi - Mg);
+      a += f * part_a[i][dsub];
+      Lg += f * part_l[i][dsub];
     }
-    float v = a / L;
-    bf16 ob = f2bf(v);
+    bf16 ob = f2bf(a / Lg);
     if (gate != nullptr) {
       // Reference gate numerics (native_pointwise.hip.cpp:207-222): sigmoid in
       // fp32, rounded to bf16, product rounded to bf16.
@@ -271,7 +291,7 @@ __global__ __launch_bounds__(256) void decode_gqa_combine_kernel(
 unsigned choose_split_tokens(unsigned cache_end) {
   // Aim for ~2 workgroups per CU-slot (256 CUs) on both KV heads while
   // keeping at least one 32-token block per wave.
-  const unsigned target_splits = 256;
+  const unsigned target_splits = kMaxSplits;
   unsigned per = (cache_end + target_splits - 1) / target_splits;
   const unsigned quantum = kDecWaves * kDecBlock;  // 128
   per = (per + quantum - 1) / quantum * quantum;
@@ -309,24 +329,19 @@ Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
     return Q36_EINVAL;
   const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
   const unsigned nsplit = (cache_end + per - 1) / per;
+  if (nsplit > kMaxSplits) return Q36_EINVAL;
   const size_t need = (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
   if (workspace_bytes < need) return Q36_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (k_new != nullptr) {
-    hipLaunchKernelGGL(write_kv_row_kernel, dim3(1), dim3(64), 0, st,
-                       static_cast<const bf16*>(k_new),
-                       static_cast<const bf16*>(v_new),
-                       static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
-                       position);
-  }
   float* ws_o = static_cast<float*>(workspace);
   float* ws_ml = ws_o + (size_t)nsplit * kHkv * kGroup * kD;
   hipLaunchKernelGGL(decode_gqa_split_kernel, dim3(nsplit, kHkv), dim3(256), 0,
                      st, static_cast<const bf16*>(q),
-                     static_cast<const bf16*>(k_cache),
-                     static_cast<const bf16*>(v_cache), cache_end, per, nsplit,
-                     ws_o, ws_ml);
-  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / 32), dim3(256),
+                     static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
+                     static_cast<const bf16*>(k_new),
+                     static_cast<const bf16*>(v_new), position, cache_end, per,
+                     nsplit, ws_o, ws_ml);
+  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / 32), dim3(512),
                      0, st, ws_o, ws_ml, nsplit, static_cast<const bf16*>(gate),
                      gate_head_stride, static_cast<bf16*>(out));
   return static_cast<int>(hipGetLastError());

@@ -39,11 +39,11 @@ SIGNATURES: dict[str, tuple] = {
     # Gated DeltaNet
     "qwen36_gdn_conv1d": (_i32, [_vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
     "qwen36_gdn_gating": (_i32, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
-    "qwen36_gdn_recurrent": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp,
-                                    _vp, _vp, _u32, _u32, _vp]),
+    "qwen36_gdn_recurrent": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
+                                    _vp, _vp, _vp, _u32, _vp]),
     "qwen36_gdn_chunk_prefill_workspace_bytes": (_sz, [_u32]),
-    "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp,
-                                        _vp, _vp, _u32, _u32, _vp, _sz, _vp]),
+    "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
+                                        _vp, _vp, _vp, _u32, _vp, _sz, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
 }
 

@@ -140,3 +140,116 @@ class FmhaProvider:
         _lib.call("qrt_ck_fmha_release")
         self._outputs.clear()
         self._prepared = False
+
+
+def rotary_table(tokens: int, position_start: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin tables [tokens, 32] for absolute positions
+    [position_start, position_start + tokens) (native_pointwise.hip.cpp:224-238)."""
+    cos = torch.empty(tokens, 32, dtype=torch.float32, device=device)
+    sin = torch.empty_like(cos)
+    _lib.call("qwen36_rotary_table", ptr(cos), ptr(sin), tokens, position_start,
+              stream_handle(cos.device))
+    return cos, sin
+
+
+def head_norm_rope_kv_write(q_gate: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                            q_norm: torch.Tensor, k_norm: torch.Tensor,
+                            k_cache: torch.Tensor, v_cache: torch.Tensor,
+                            position_start: int, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Head RMSNorm (w+1) + partial RoPE for the 16 query heads (read from the
+    fused [Q|Gate] rows of ``q_gate`` [T, 8192]) and the 2 key heads ([T, 512]);
+    K and the raw V are written to cache rows [position_start, +T)
+    (four_layer_mini_engine.py:6566-6573 + 5151-5162 + 5980-5986).
+    Returns q [T, 16, 256] bf16."""
+    t = q_gate.shape[0]
+    for name, x, width in (("q_gate", q_gate, 2 * Q_DIM), ("k", k, KV_DIM), ("v", v, KV_DIM)):
+        require(x, name, torch.bfloat16, contiguous=False)
+        if x.dim() != 2 or x.shape[0] != t or x.shape[1] != width or x.stride(1) != 1:
+            raise ValueError(f"{name} must be [T, {width}] with unit inner stride")
+    require(q_norm, "q_norm", torch.bfloat16, shape=(HEAD_DIM,))
+    require(k_norm, "k_norm", torch.bfloat16, shape=(HEAD_DIM,))
+    require(k_cache, "k_cache", torch.bfloat16)
+    require(v_cache, "v_cache", torch.bfloat16)
+    if position_start + t > k_cache.shape[0]:
+        raise ValueError("cache too small for the new rows")
+    if q_out is None:
+        q_out = torch.empty(t, HQ, HEAD_DIM, dtype=torch.bfloat16, device=q_gate.device)
+    _lib.call("qwen36_head_norm_rope", ptr(q_gate), q_gate.stride(0), ptr(k), k.stride(0),
+              ptr(v), v.stride(0), ptr(q_norm), ptr(k_norm), t, position_start,
+              ptr(q_out), ptr(k_cache), ptr(v_cache), stream_handle(q_gate.device))
+    return q_out
+
+
+def output_gate(attn: torch.Tensor, q_gate: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """``attn * sigmoid(gate)`` with the gate half of the fused q-projection
+    rows (four_layer_mini_engine.py:6650; native_pointwise.hip.cpp:207-222 and
+    :339-359 for fp32 attention).  attn [T, 4096] bf16 or fp32."""
+    t = attn.shape[0]
+    if attn.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("attn must be bf16 or fp32")
+    require(attn, "attn", attn.dtype, shape=(t, Q_DIM))
+    require(q_gate, "q_gate", torch.bfloat16, contiguous=False)
+    if q_gate.shape != (t, 2 * Q_DIM) or q_gate.stride(1) != 1:
+        raise ValueError("q_gate must be [T, 8192] with unit inner stride")
+    if out is None:
+        out = torch.empty(t, Q_DIM, dtype=torch.bfloat16, device=attn.device)
+    _lib.call("qwen36_output_gate", ptr(attn), int(attn.dtype == torch.float32), ptr(q_gate),
+              q_gate.stride(0), ptr(out), t, stream_handle(attn.device))
+    return out
+
+
+class FullAttentionLayer:
+    """One gated GQA layer with its resident KV cache, mirroring
+    ``full_attention(inp, layer_index, weights)``
+    (four_layer_mini_engine.py:6546-6653).
+
+    Projections use torch matmul (they are outside the attention hot path);
+    head-norm + RoPE + KV write, the attention core (FMHA provider for
+    prefill, split-K decode) and the output gate run in the HIP library.
+    ``weights``: q_proj [8192,2048], k_proj/v_proj [512,2048],
+    o_proj [2048,4096], q_norm/k_norm [256] (all bf16 on the GPU)."""
+
+    def __init__(self, weights: dict, capacity: int, device) -> None:
+        self.w = weights
+        self.capacity = capacity
+        self.k_cache = torch.zeros(capacity, HKV, HEAD_DIM, dtype=torch.bfloat16, device=device)
+        self.v_cache = torch.zeros_like(self.k_cache)
+
+    def forward(self, inp: torch.Tensor, position_start: int, mode: str) -> torch.Tensor:
+        t = inp.shape[0]
+        if position_start + t > self.capacity:
+            raise ValueError("KV cache capacity exceeded")
+        w = self.w
+        q_gate = inp @ w["q_proj"].t()
+        k = inp @ w["k_proj"].t()
+        v = inp @ w["v_proj"].t()
+        cache_end = position_start + t
+        if mode == "decode":
+            if t != 1:
+                raise ValueError("decode takes one token")
+            # norm+rope writes K into the cache row; the decode core then needs no k_new.
+            q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
+                                        self.k_cache, self.v_cache, position_start)
+            gate = q_gate.view(HQ, 2 * HEAD_DIM)[:, HEAD_DIM:]
+            attn = _decode_with_strided_gate(q, self.k_cache, self.v_cache, cache_end, gate)
+        else:
+            q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
+                                        self.k_cache, self.v_cache, position_start)
+            attn32 = fmha_prefill(q, self.k_cache[:cache_end], self.v_cache[:cache_end])
+            attn = output_gate(attn32, q_gate)
+        return attn @ w["o_proj"].t()
+
+
+def _decode_with_strided_gate(q, k_cache, v_cache, cache_end, gate_view):
+    """Decode core with the gate read in place from the fused q projection
+    (head stride 512)."""
+    dev = q.device
+    out = torch.empty(1, Q_DIM, dtype=torch.bfloat16, device=dev)
+    lib = _lib.load(("qwen36_decode_gqa",))
+    ws_bytes = lib.qwen36_decode_gqa_workspace_bytes(cache_end, 0)
+    ws = scratch("decode_gqa", ws_bytes, dev)
+    _lib.call("qwen36_decode_gqa", ptr(q), None, None, ptr(k_cache), ptr(v_cache),
+              cache_end - 1, cache_end, k_cache.shape[0], gate_view.data_ptr(),
+              gate_view.stride(0), ptr(out), ptr(ws), ws.numel(), 0, stream_handle(dev))
+    return out

@@ -1,0 +1,196 @@
+"""Host-side mirror of the reference's Gated-DeltaNet (linear attention) path.
+
+Reference interfaces mirrored (four_layer_mini_engine.py, "fle"):
+  * ``linear_attention(inp, layer_index, weights)`` -- fle:6378-6544
+  * ``linear_causal_conv`` -- fle:5293-5403
+  * ``torch_chunk_gated_delta_rule(query, key, value, g, beta, initial_state,
+    chunk_size=64)`` -- fle:5167-5240
+  * ``torch_recurrent_gated_delta_rule(query, key, value, g, beta,
+    initial_state)`` -- fle:5242-5276
+  * gated RMSNorm -- fle:6531-6541
+All arithmetic runs in ``libqwen36_attn.so``.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._tensors import ptr, require, scratch, stream_handle
+
+HK, HV, DK, DV = 16, 32, 128, 128
+KEY_DIM, VALUE_DIM = HK * DK, HV * DV
+CONV_DIM = 2 * KEY_DIM + VALUE_DIM
+CHUNK = 64
+
+
+def causal_conv1d(mixed_qkv: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
+                  new_state: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Depthwise causal conv (k=4) + SiLU over [state | x].  mixed_qkv [T, 8192]
+    bf16 (unit inner stride), conv_state [8192, 3] bf16, weight [8192, 4] bf16.
+    Returns (out [T, 8192] bf16, new_state [8192, 3]); ``new_state`` may be
+    ``conv_state`` itself (in-place update)."""
+    t = mixed_qkv.shape[0]
+    require(mixed_qkv, "mixed_qkv", torch.bfloat16, contiguous=False)
+    if mixed_qkv.shape[1] != CONV_DIM or mixed_qkv.stride(1) != 1:
+        raise ValueError("mixed_qkv must be [T, 8192] with unit inner stride")
+    require(conv_state, "conv_state", torch.bfloat16, shape=(CONV_DIM, 3))
+    require(weight, "weight", torch.bfloat16, shape=(CONV_DIM, 4))
+    if new_state is None:
+        new_state = torch.empty_like(conv_state)
+    if out is None:
+        out = torch.empty(t, CONV_DIM, dtype=torch.bfloat16, device=mixed_qkv.device)
+    _lib.call("qwen36_gdn_conv1d", ptr(mixed_qkv), mixed_qkv.stride(0), ptr(weight),
+              ptr(conv_state), ptr(new_state), ptr(out), t, stream_handle(out.device))
+    return out, new_state
+
+
+def gating(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+           dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b); fp32 [T, 32]
+    (fle:6507-6511)."""
+    t = a.shape[0]
+    for name, x in (("a", a), ("b", b)):
+        require(x, name, torch.bfloat16, contiguous=False)
+        if x.shape != (t, HV) or x.stride(1) != 1:
+            raise ValueError(f"{name} must be [T, 32]")
+    if a.stride(0) != b.stride(0):
+        raise ValueError("a and b must share a row stride")
+    a_log = a_log.float().contiguous()
+    dt_bias = dt_bias.float().contiguous()
+    g = torch.empty(t, HV, dtype=torch.float32, device=a.device)
+    beta = torch.empty_like(g)
+    _lib.call("qwen36_gdn_gating", ptr(a), ptr(b), a.stride(0), ptr(a_log), ptr(dt_bias),
+              ptr(g), ptr(beta), t, stream_handle(a.device))
+    return g, beta
+
+
+def _qkv_views(query, key, value):
+    """Accept [T,H,128] or [1,T,H,128] q/k (H = 16 unrepeated or 32 repeated)
+    and v [T,32,128] / [1,T,32,128]; return strides for the C ABI."""
+    def squeeze(x, name):
+        if x.dim() == 4:
+            if x.shape[0] != 1:
+                raise ValueError(f"{name}: batch must be 1")
+            x = x[0]
+        if x.dim() != 3:
+            raise ValueError(f"{name} must be [T, H, 128]")
+        require(x, name, torch.bfloat16, contiguous=False)
+        if x.stride(2) != 1 or x.stride(1) != x.shape[2]:
+            raise ValueError(f"{name} must have contiguous heads")
+        return x
+    q, k, v = squeeze(query, "query"), squeeze(key, "key"), squeeze(value, "value")
+    t, hq = q.shape[0], q.shape[1]
+    if k.shape != q.shape or q.stride(0) != k.stride(0):
+        raise ValueError("query and key must share shape and token stride")
+    if hq not in (HK, HV) or q.shape[2] != DK:
+        raise ValueError("query/key must have 16 or 32 heads of 128")
+    if v.shape != (t, HV, DV):
+        raise ValueError("value must be [T, 32, 128]")
+    return q, k, v, t, hq
+
+
+def _gb(g, beta, t):
+    g = g.reshape(t, HV)
+    beta = beta.reshape(t, HV)
+    require(g, "g", torch.float32)
+    require(beta, "beta", torch.float32)
+    return g, beta
+
+
+def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state,
+                               final_state: torch.Tensor | None = None):
+    """Mirror of ``torch_recurrent_gated_delta_rule`` (fle:5242-5276) with the
+    l2norm of q/k done in-kernel.  initial_state [32,128,128] (or [1,...]) fp32
+    in [H, dk, dv] orientation.  Returns (out [1,T,32,128] bf16, final_state);
+    ``final_state`` may alias ``initial_state``."""
+    q, k, v, t, hq = _qkv_views(query, key, value)
+    g, beta = _gb(g, beta, t)
+    s_in = initial_state.reshape(HV, DK, DV)
+    require(s_in, "initial_state", torch.float32)
+    if final_state is None:
+        final_state = torch.empty_like(s_in)
+    out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=q.device)
+    _lib.call("qwen36_gdn_recurrent", ptr(q), ptr(k), ptr(v), hq, q.stride(0), v.stride(0),
+              ptr(g), ptr(beta), ptr(s_in), ptr(final_state), ptr(out), t,
+              stream_handle(q.device))
+    return out, final_state.view(1, HV, DK, DV)
+
+
+def chunk_gated_delta_rule(query, key, value, g, beta, initial_state=None, chunk_size: int = CHUNK,
+                           final_state: torch.Tensor | None = None):
+    """Mirror of ``torch_chunk_gated_delta_rule`` (fle:5167-5240); chunk 64.
+    ``initial_state`` None means zeros.  Returns (out [1,T,32,128] bf16,
+    final_state [1,32,128,128] fp32)."""
+    if chunk_size != CHUNK:
+        raise ValueError("the HIP kernel implements chunk_size=64")
+    q, k, v, t, hq = _qkv_views(query, key, value)
+    g, beta = _gb(g, beta, t)
+    s_in = None
+    if initial_state is not None:
+        s_in = initial_state.reshape(HV, DK, DV)
+        require(s_in, "initial_state", torch.float32)
+    if final_state is None:
+        final_state = torch.empty(HV, DK, DV, dtype=torch.float32, device=q.device)
+    out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=q.device)
+    lib = _lib.load(("qwen36_gdn_chunk_prefill",))
+    nb = lib.qwen36_gdn_chunk_prefill_workspace_bytes(t)
+    ws = scratch("gdn_chunk", nb, q.device)
+    _lib.call("qwen36_gdn_chunk_prefill", ptr(q), ptr(k), ptr(v), hq, q.stride(0), v.stride(0),
+              ptr(g), ptr(beta), ptr(s_in), ptr(final_state), ptr(out), t, ptr(ws), ws.numel(),
+              stream_handle(q.device))
+    return out, final_state.view(1, HV, DK, DV)
+
+
+def gated_rmsnorm(core: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """fle:6531-6541: rmsnorm_128(core) * w -> bf16 -> * SiLU(z) -> bf16.
+    core [T,32,128] (or [1,T,32,128]) bf16, z [T,4096]; returns [T, 4096]."""
+    core = core.reshape(-1, HV, DV)
+    t = core.shape[0]
+    require(core, "core", torch.bfloat16)
+    require(z, "z", torch.bfloat16, contiguous=False)
+    if z.shape != (t, VALUE_DIM) or z.stride(1) != 1:
+        raise ValueError("z must be [T, 4096] with unit inner stride")
+    require(weight, "weight", torch.bfloat16, shape=(DV,))
+    out = torch.empty(t, VALUE_DIM, dtype=torch.bfloat16, device=core.device)
+    _lib.call("qwen36_gdn_gated_norm", ptr(core), ptr(z), z.stride(0), ptr(weight), ptr(out), t,
+              stream_handle(core.device))
+    return out
+
+
+class LinearAttentionLayer:
+    """One Gated-DeltaNet layer with its carried conv and recurrent states,
+    mirroring ``linear_attention(inp, layer_index, weights)``
+    (fle:6378-6544, plain-torch branch).  Projections are torch matmuls (outside
+    the hot path); conv, gating, delta rule and gated norm run in the HIP
+    library.  ``weights``: in_proj_qkv [8192,2048], in_proj_z [4096,2048],
+    in_proj_a/in_proj_b [32,2048], conv1d [8192,4], A_log [32], dt_bias [32],
+    norm [128], out_proj [2048,4096]."""
+
+    def __init__(self, weights: dict, device) -> None:
+        self.w = weights
+        self.conv_state = torch.zeros(CONV_DIM, 3, dtype=torch.bfloat16, device=device)
+        self.ssm_state = torch.zeros(HV, DK, DV, dtype=torch.float32, device=device)
+
+    def forward(self, inp: torch.Tensor, mode: str) -> torch.Tensor:
+        w = self.w
+        mixed = inp @ w["in_proj_qkv"].t()
+        z = inp @ w["in_proj_z"].t()
+        b = inp @ w["in_proj_b"].t()
+        a = inp @ w["in_proj_a"].t()
+        conv_out, _ = causal_conv1d(mixed, self.conv_state, w["conv1d"], new_state=self.conv_state)
+        t = conv_out.shape[0]
+        q = conv_out[:, :KEY_DIM].view(t, HK, DK)
+        k = conv_out[:, KEY_DIM:2 * KEY_DIM].view(t, HK, DK)
+        v = conv_out[:, 2 * KEY_DIM:].view(t, HV, DV)
+        g, beta = gating(a, b, w["A_log"], w["dt_bias"])
+        if mode == "decode":
+            core, _ = recurrent_gated_delta_rule(q, k, v, g, beta, self.ssm_state,
+                                                 final_state=self.ssm_state)
+        else:
+            new_state = torch.empty_like(self.ssm_state)
+            core, _ = chunk_gated_delta_rule(q, k, v, g, beta, self.ssm_state,
+                                             final_state=new_state)
+            self.ssm_state = new_state
+        gated = gated_rmsnorm(core, z, w["norm"])
+        return gated @ w["out_proj"].t()

