@@ -164,6 +164,53 @@ def bench_prefill(torch, fa, dev, t, s, iters, warmup, seed=1):
             "frac_bf16_mfma": tf / BF16_PEAK_TFLOPS}
 
 
+GDN_STATE_BYTES = 2 * 32 * 128 * 128 * 4     # fp32 state read + write per layer step
+GDN_LAYERS = 30
+
+
+def bench_gdn_recurrent(torch, dev, layers, iters, warmup, use_graph, seed=2):
+    """Config 5 GDN part: one recurrent decode step through 30 layers, each
+    with its own fp32 state (state updated in place)."""
+    from qwen36_attn import _lib
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(seed)
+    q, k, v, gg, beta = [x.to(dev) for x in syn.gdn_core_inputs(layers, g, a_max=16.0)]
+    states = [torch.randn(32, 128, 128, generator=g).to(dev) for _ in range(layers)]
+    outs = [torch.empty(1, 32, 128, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+
+    def step():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(layers):
+            _lib.call("qwen36_gdn_recurrent", q[i].data_ptr(), k[i].data_ptr(), v[i].data_ptr(),
+                      16, 2048, 4096, gg[i].data_ptr(), beta[i].data_ptr(), states[i].data_ptr(),
+                      states[i].data_ptr(), outs[i].data_ptr(), 1, st)
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    nbytes = GDN_STATE_BYTES * layers
+    return {"layers": layers, "us_per_token": us, "hbm_gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_gdn_prefill(torch, dev, t, iters, warmup, seed=3):
+    """Config 4: chunked delta-rule prefill of T tokens from zero state."""
+    from qwen36_attn import gated_deltanet as G
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(seed)
+    q, k, v, gg, beta = [x.to(dev) for x in syn.gdn_core_inputs(t, g, a_max=16.0)]
+    fs = torch.empty(32, 128, 128, dtype=torch.float32, device=dev)
+    ms = Timer(torch).time(lambda: G.chunk_gated_delta_rule(q, k, v, gg, beta, None, final_state=fs),
+                           iters, warmup)
+    c = 64
+    flop_per_unit = 6 * 2 * c * c * 128 + 4 * 2 * c * 128 * 128 + c ** 3 // 3
+    flop = flop_per_unit * (t // c) * 32
+    nbytes = 2 * t * 16 * 128 * 2 + t * 32 * 128 * 2 * 2 + t * 32 * 4 * 2 + 32 * 128 * 128 * 4
+    return {"tokens": t, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
+            "frac_fp32_mfma": flop / (ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
+            "frac_bf16_mfma": flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "hbm_gbs_algorithmic": nbytes / (ms * 1e-3) / 1e9}
+
+
 def cpu_baseline(torch, cache_end):
     """Oracle grouped bf16 decode on this host's cores: a bounded sample of
     whole layers at the headline cache length, scaled to the 10-layer step."""
@@ -210,7 +257,11 @@ def main():
         "decode_262143": bench_decode(torch, fa, dev, 262143, N_FULL_LAYERS, 10, 2, use_graph),
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
+        "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
+        "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
     }
+    extra["attention_us_per_token_128k"] = (head["us_per_token"]
+                                            + extra["gdn_recurrent_30layers"]["us_per_token"])
     torch.cuda.empty_cache()
     # Roofline of the dominant kernel (split-K decode), per layer launch.
     per_layer_us = head["us_per_token"] / N_FULL_LAYERS

@@ -1,0 +1,94 @@
+"""CPU checks: the C-ABI library exports every symbol declared in
+include/qwen36_attn.h and rejects bad arguments before touching the GPU; the
+committed golden fixtures still match the oracle."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+from safetensors.torch import load_file
+
+from oracle import attention_oracle as O
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwen36_attn.h")
+FIXTURES = os.path.join(ROOT, "tests", "golden", "fixtures.safetensors")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from qwen36_attn import _lib
+    if not os.path.isfile(_lib.library_path()):
+        pytest.skip("library not built")
+    return ctypes.CDLL(_lib.library_path())
+
+
+def test_header_lists_expected_entry_points():
+    syms = header_symbols()
+    assert "qrt_ck_fmha_bf16_launch_ex" in syms and "qwen36_decode_gqa" in syms
+    assert len(syms) >= 18
+
+
+def test_library_exports_every_header_symbol(lib):
+    missing = [s for s in header_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_binding_table_matches_header():
+    from qwen36_attn import _lib
+    assert sorted(_lib.SIGNATURES) == header_symbols()
+
+
+def test_bad_arguments_rejected_without_launch(lib):
+    from qwen36_attn import _lib
+    L = _lib.load()
+    assert L.qrt_ck_fmha_prepare(0) == 1
+    assert L.qrt_ck_fmha_prepare(262145) == 1
+    assert L.qrt_ck_fmha_prepare(1) == 0
+    assert L.qrt_ck_fmha_release() == 0
+    # null pointers / kv < q / oversize: hipErrorInvalidValue, nothing launched
+    assert L.qrt_ck_fmha_bf16_launch(None, None, None, None, 16, None) == 1
+    assert L.qrt_ck_fmha_bf16_launch_ex(1, 1, 1, 1, 8, 4, None) == 1
+    assert L.qrt_ck_fmha_bf16_launch_ex(1, 1, 1, 1, 8, 262145, None) == 1
+    assert L.qwen36_decode_gqa(None, None, None, None, None, 0, 1, 1, None, 0, None, None, 0, 0, None) == 1
+    # cache_end beyond capacity
+    assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 9, 8, None, 0, 1, 1, 1 << 20, 0, None) == 1
+    # k_new without v_new
+    assert L.qwen36_decode_gqa(1, 1, None, 1, 1, 0, 8, 8, None, 0, 1, 1, 1 << 20, 0, None) == 1
+    # split_tokens not a multiple of 128
+    assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 8, 8, None, 0, 1, 1, 1 << 20, 100, None) == 1
+    # workspace too small
+    assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 4096, 4096, None, 0, 1, 1, 16, 0, None) == 1
+    assert L.qwen36_decode_gqa_workspace_bytes(0, 0) == 0
+    assert L.qwen36_decode_gqa_workspace_bytes(131072, 0) > 0
+    assert L.qwen36_gdn_recurrent(1, 1, 1, 8, 2048, 4096, 1, 1, 1, 1, 1, 1, None) == 1  # qk_heads
+    assert L.qwen36_gdn_chunk_prefill(1, 1, 1, 16, 2048, 4096, 1, 1, None, 1, 1, 64, 1, 0, None) == 1
+    assert L.qwen36_gdn_conv1d(1, 100, 1, 1, 1, 1, 4, None) == 1  # row stride < 8192
+    assert L.qwen36_head_norm_rope(1, 8192, 1, 512, 1, 512, 1, 1, 0, 0, 1, 1, 1, None) == 1
+    assert L.qwen36_output_gate(1, 0, 1, 100, 1, 1, None) == 1
+    assert L.qwen36_rotary_table(None, None, 1, 0, None) == 1
+    assert L.qwen36_gdn_gated_norm(1, 1, 100, 1, 1, 1, None) == 1
+    assert L.qwen36_gdn_gating(1, 1, 8, 1, 1, 1, 1, 1, None) == 1
+
+
+def test_fixtures_match_oracle():
+    from tests.golden.make_fixtures import build
+    fresh = build()
+    saved = load_file(FIXTURES)
+    assert sorted(fresh) == sorted(saved)
+    for k, v in saved.items():
+        assert torch.equal(fresh[k], v), k
+
+
+def test_fixture_prefill_is_tail_of_decode_chain():
+    f = load_file(FIXTURES)
+    # The bf16 prefill output's last row equals a decode of that row over all 9 keys.
+    dec = O.decode_attention_grouped_bf16(f["prefill.q"][-1:], f["prefill.k"], f["prefill.v"], 9)
+    assert (dec.float() - f["prefill.out_f32"][-1:]).abs().max() <= 2e-2

@@ -1,0 +1,283 @@
+"""CPU checks that pin the oracle restatement (oracle/attention_oracle.py)
+independently of its own text: reference-held constants, closed forms,
+brute force in fp64 on tiny shapes, and invariants chosen so that a dropped
+term, wrong sign/index or transposed operand fails.
+
+Which check pins which function:
+  inv_freq / rope_cos_sin   -> reference KAT table; closed-form rotation
+  head_rmsnorm              -> fp64 formula; (w+1) convention (w=-1 -> 0)
+  apply_rope                -> fp64 rotation, position 0 identity, norm
+  prefill_attention         -> fp64 brute force with explicit mask loops;
+                               GQA == MHA on repeated KV; prefix extension
+  decode_attention_*        -> last row of prefill; fp64 brute force
+  output_gate               -> sigmoid(0) = 1/2 exact; fp64 formula
+  causal_conv1d             -> F.conv1d groups=C; state carry
+  l2norm / gdn_gating       -> unit norms; fp64 closed form
+  chunk/recurrent delta rule-> fp64 brute-force recurrence; chunked ==
+                               recurrent; beta=0 pure decay; one step from
+                               zero state; state carry across calls
+  gated_rmsnorm             -> fp64 formula; weight without +1
+  full_attention layer      -> prefill(T) + decode == prefill(T+1) tail
+"""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention_oracle as O
+from tests.golden.rope_table import INV_FREQ_KAT
+
+torch.manual_seed(0)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def test_inv_freq_matches_reference_table():
+    got = O.inv_freq()
+    kat = torch.tensor(INV_FREQ_KAT, dtype=torch.float32)
+    assert torch.allclose(got, kat, rtol=3e-7, atol=0)
+    exact = torch.tensor([1.0 / math.pow(1e7, 2 * i / 64) for i in range(32)], dtype=torch.float64)
+    assert torch.allclose(kat.double(), exact, rtol=1e-7)
+
+
+def test_rope_cos_sin_and_rotation():
+    cos, sin = O.rope_cos_sin(5, 3)
+    assert cos.shape == (3, 1, 32)
+    pos = torch.tensor([5.0, 6.0, 7.0], dtype=torch.float64)
+    ang = pos[:, None] * torch.tensor(INV_FREQ_KAT, dtype=torch.float64)[None]
+    assert torch.allclose(cos[:, 0].double(), torch.cos(ang), atol=2e-6)
+    assert torch.allclose(sin[:, 0].double(), torch.sin(ang), atol=2e-6)
+    x = torch.randn(3, 2, 256, generator=gen(1)).to(torch.bfloat16)
+    y = O.apply_rope(x, cos, sin)
+    # dims >= 64 untouched; pair (i, i+32) rotated by angle i
+    assert torch.equal(y[..., 64:], x[..., 64:])
+    xf = x.double()
+    a, b = xf[..., :32], xf[..., 32:64]
+    c, s = torch.cos(ang)[:, None], torch.sin(ang)[:, None]
+    ref = torch.cat((a * c - b * s, b * c + a * s), -1)
+    assert (y[..., :64].double() - ref).abs().max() <= 0.02
+    # position 0 is the identity
+    c0, s0 = O.rope_cos_sin(0, 3)
+    y0 = O.apply_rope(x, c0[:1].expand(3, 1, 32), s0[:1].expand(3, 1, 32))
+    assert torch.equal(y0, x)
+
+
+def test_head_rmsnorm_formula_and_plus_one():
+    x = torch.randn(4, 3, 256, generator=gen(2)).to(torch.bfloat16)
+    w = torch.randn(256, generator=gen(3)).to(torch.bfloat16)
+    y = O.head_rmsnorm(x, w)
+    xd = x.double()
+    ref = xd / torch.sqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6) * (w.double() + 1)
+    assert (y.double() - ref).abs().max() <= 2 ** -8 * ref.abs().max()
+    assert torch.count_nonzero(O.head_rmsnorm(x, -torch.ones(256, dtype=torch.bfloat16))) == 0
+
+
+def brute_attention(q, k, v, position_start):
+    """fp64, explicit loops over query rows: softmax(q k^T / sqrt(D)) v with
+    key j visible to query i iff j <= i + position_start; head h -> kv h // 8."""
+    t, hq, d = q.shape
+    out = torch.zeros(t, hq, d, dtype=torch.float64)
+    for h in range(hq):
+        kv = h // (hq // k.shape[1])
+        for i in range(t):
+            lim = i + position_start + 1
+            s = (k[:lim, kv].double() @ q[i, h].double()) / math.sqrt(d)
+            p = torch.softmax(s, 0)
+            out[i, h] = p @ v[:lim, kv].double()
+    return out.reshape(t, hq * d)
+
+
+@pytest.mark.parametrize("t,s", [(1, 1), (5, 5), (3, 9), (17, 17), (4, 40)])
+def test_prefill_attention_brute_force(t, s):
+    g = gen(t * 100 + s)
+    q = torch.randn(t, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    ref = brute_attention(q, k, v, s - t)
+    got32 = O.prefill_attention(q, k, v, s - t, out_dtype=torch.float32)
+    assert (got32.double() - ref).abs().max() <= 1e-5
+    got16 = O.prefill_attention(q, k, v, s - t)
+    assert (got16.double() - ref).abs().max() <= 2e-2
+
+
+def test_prefill_gqa_equals_mha_and_prefix_extension():
+    g = gen(9)
+    s, t = 40, 12
+    q = torch.randn(s, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    full = O.prefill_attention(q, k, v, 0, out_dtype=torch.float32)
+    tail = O.prefill_attention(q[s - t:], k, v, s - t, out_dtype=torch.float32)
+    assert torch.allclose(full[s - t:], tail, atol=1e-6)
+    # GQA vs explicit per-head MHA with K/V repeated 8x
+    kr = k.repeat_interleave(8, dim=1)
+    vr = v.repeat_interleave(8, dim=1)
+    mha = F.scaled_dot_product_attention(q.float().transpose(0, 1), kr.float().transpose(0, 1),
+                                         vr.float().transpose(0, 1), is_causal=True)
+    assert torch.allclose(full, mha.transpose(0, 1).reshape(s, 4096), atol=1e-5)
+
+
+def test_decode_is_last_row_of_prefill():
+    g = gen(10)
+    s = 33
+    q = torch.randn(s, 16, 256, generator=g).to(torch.bfloat16)
+    k = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    v = torch.randn(s, 2, 256, generator=g).to(torch.bfloat16)
+    pre = O.prefill_attention(q, k, v, 0, out_dtype=torch.float32)
+    dec32 = O.decode_attention_f32(q[-1:], k, v, s)
+    assert torch.allclose(pre[-1:], dec32, atol=1e-5)
+    dec16 = O.decode_attention_grouped_bf16(q[-1:], k, v, s)
+    assert (dec16.float() - dec32).abs().max() <= 2e-2
+    # cache_end restricts the keys: same as a shorter cache
+    assert torch.allclose(O.decode_attention_f32(q[-1:], k, v, 20),
+                          O.decode_attention_f32(q[-1:], k[:20], v[:20], 20))
+
+
+def test_output_gate_sigmoid_half():
+    attn = torch.randn(2, 4096, generator=gen(11)).to(torch.bfloat16)
+    assert torch.equal(O.output_gate(attn, torch.zeros(2, 4096, dtype=torch.bfloat16)),
+                       attn * 0.5)
+    gate = torch.randn(2, 4096, generator=gen(12)).to(torch.bfloat16)
+    ref = attn.double() / (1 + torch.exp(-gate.double()))
+    assert (O.output_gate(attn, gate).double() - ref).abs().max() <= 2e-2
+
+
+def test_split_q_gate_layout():
+    qg = torch.arange(2 * 8192, dtype=torch.float32).view(2, 8192)
+    q, gate = O.split_q_gate(qg)
+    assert q[1, 3, 0].item() == 8192 + 3 * 512
+    assert gate[1, 3 * 256].item() == 8192 + 3 * 512 + 256
+
+
+def test_causal_conv1d_textbook_and_carry():
+    g = gen(13)
+    c = 8192
+    x = torch.randn(10, c, generator=g).to(torch.bfloat16)
+    w = (torch.randn(c, 4, generator=g) * 0.5).to(torch.bfloat16)
+    z = torch.zeros(c, 3, dtype=torch.bfloat16)
+    out, st = O.causal_conv1d(x, z, w)
+    ref = F.conv1d(x.t().unsqueeze(0).double(), w.double().unsqueeze(1), padding=3, groups=c)[..., :10]
+    ref = F.silu(ref).squeeze(0).t()
+    # two bf16 roundings (conv, then SiLU): <= 2 * 2^-9 relative
+    assert ((out.double() - ref).abs() <= 2 ** -7 * ref.abs() + 1e-3).all()
+    assert torch.equal(st, x[-3:].t().contiguous())
+    o1, s1 = O.causal_conv1d(x[:4], z, w)
+    o2, s2 = O.causal_conv1d(x[4:], s1, w)
+    assert torch.equal(torch.cat((o1, o2)), out) and torch.equal(s2, st)
+    # T < 3 keeps part of the old state
+    o3, s3 = O.causal_conv1d(x[:1], st, w)
+    assert torch.equal(s3, torch.cat((st[:, 1:], x[:1].t()), 1))
+
+
+def test_l2norm_and_gating():
+    x = torch.randn(7, 128, generator=gen(14))
+    n = O.l2norm(x).norm(dim=-1)
+    assert torch.allclose(n, torch.ones(7), atol=1e-5)
+    a = torch.randn(5, 32, generator=gen(15)).to(torch.bfloat16)
+    b = torch.randn(5, 32, generator=gen(16)).to(torch.bfloat16)
+    a_log = torch.randn(32, generator=gen(17))
+    dt = torch.randn(32, generator=gen(18))
+    g, beta = O.gdn_gating(a, b, a_log, dt)
+    ref_g = -torch.exp(a_log.double()) * torch.log1p(torch.exp(a.double() + dt.double()))
+    assert torch.allclose(g.double(), ref_g, rtol=1e-5)
+    assert torch.allclose(beta.double(), torch.sigmoid(b.double()), rtol=1e-6)
+
+
+def brute_delta_rule(q, k, v, g, beta, s0):
+    """fp64 textbook gated delta rule, token by token, per head.
+    q,k [T,H,dk] (raw), v [T,H,dv], g,beta [T,H], s0 [H,dk,dv]."""
+    q = q.double()
+    k = k.double()
+    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6) / math.sqrt(q.shape[-1])
+    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    s = s0.double().clone()
+    outs = []
+    for t in range(q.shape[0]):
+        s = s * torch.exp(g[t].double())[:, None, None]
+        pred = torch.einsum("hkv,hk->hv", s, k[t])
+        delta = (v[t].double() - pred) * beta[t].double()[:, None]
+        s = s + torch.einsum("hk,hv->hkv", k[t], delta)
+        outs.append(torch.einsum("hkv,hk->hv", s, q[t]))
+    return torch.stack(outs), s
+
+
+def _gdn_inputs(t, h, seed, a_max=1.0):
+    g = gen(seed)
+    q = torch.randn(t, h, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(t, h, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(t, h, 128, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(t, h, generator=g))
+    gg = -F.softplus(torch.randn(t, h, generator=g)) * (torch.rand(h, generator=g) * a_max)
+    s0 = torch.randn(h, 128, 128, generator=g)
+    return q, k, v, gg, beta, s0
+
+
+@pytest.mark.parametrize("t", [1, 7, 64, 70])
+def test_delta_rules_match_brute_force(t):
+    q, k, v, gg, beta, s0 = _gdn_inputs(t, 3, seed=t)
+    ref_o, ref_s = brute_delta_rule(q, k, v, gg, beta, s0)
+    b = lambda x: x.unsqueeze(0)
+    ro, rs = O.recurrent_gated_delta_rule(b(q), b(k), b(v), b(gg), b(beta), b(s0))
+    co, cs = O.chunk_gated_delta_rule(b(q), b(k), b(v), b(gg), b(beta), b(s0))
+    for o, s in ((ro, rs), (co, cs)):
+        assert (o[0].double() - ref_o).abs().max() <= 2e-2
+        assert ((s[0].double() - ref_s).norm() / ref_s.norm()) <= 1e-5
+
+
+def test_chunk_size_invariance_and_carry():
+    q, k, v, gg, beta, s0 = _gdn_inputs(100, 2, seed=5)
+    b = lambda x: x.unsqueeze(0)
+    o64, s64 = O.chunk_gated_delta_rule(b(q), b(k), b(v), b(gg), b(beta), b(s0), 64)
+    for c in (16, 32):
+        oc, sc = O.chunk_gated_delta_rule(b(q), b(k), b(v), b(gg), b(beta), b(s0), c)
+        assert (oc.float() - o64.float()).abs().max() <= 2e-2
+        assert ((sc - s64).norm() / s64.norm()) <= 1e-5
+    o1, s1 = O.chunk_gated_delta_rule(b(q[:37]), b(k[:37]), b(v[:37]), b(gg[:37]), b(beta[:37]), b(s0))
+    o2, s2 = O.chunk_gated_delta_rule(b(q[37:]), b(k[37:]), b(v[37:]), b(gg[37:]), b(beta[37:]), s1)
+    assert (torch.cat((o1, o2), 1).float() - o64.float()).abs().max() <= 2e-2
+    assert ((s2 - s64).norm() / s64.norm()) <= 1e-5
+
+
+def test_delta_rule_special_cases():
+    q, k, v, gg, beta, s0 = _gdn_inputs(6, 2, seed=6)
+    b = lambda x: x.unsqueeze(0)
+    # beta = 0: the state only decays; o = (q * e^{G}) S0 with G the cumsum
+    ro, rs = O.recurrent_gated_delta_rule(b(q), b(k), b(v), b(gg), b(torch.zeros_like(beta)), b(s0))
+    decay = torch.exp(gg.sum(0))
+    assert torch.allclose(rs[0], s0 * decay[:, None, None], rtol=1e-5, atol=1e-6)
+    # one step from the zero state: S = beta k (x) v with k l2-normalised
+    zo, zs = O.recurrent_gated_delta_rule(b(q[:1]), b(k[:1]), b(v[:1]), b(gg[:1]), b(beta[:1]),
+                                          torch.zeros(1, 2, 128, 128))
+    kn = O.l2norm(k[0])
+    ref = beta[0][:, None, None] * kn[:, :, None] * v[0].float()[:, None, :]
+    assert torch.allclose(zs[0], ref, atol=1e-6)
+
+
+def test_gated_rmsnorm_formula():
+    core = torch.randn(3, 32, 128, generator=gen(19)).to(torch.bfloat16)
+    z = torch.randn(3, 4096, generator=gen(20)).to(torch.bfloat16)
+    w = torch.randn(128, generator=gen(21)).to(torch.bfloat16)
+    got = O.gated_rmsnorm(core, z, w)
+    cd = core.double().reshape(-1, 128)
+    ref = cd / torch.sqrt(cd.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+    ref = ref.reshape(3, 4096) * F.silu(z.double())
+    assert (got.double() - ref).abs().max() <= 3e-2 * max(1.0, ref.abs().max().item() / 4)
+
+
+def test_full_attention_prefill_decode_consistency():
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(22)
+    w = syn.full_attention_weights(g)
+    x = syn.randn((9, 2048), g, 0.5)
+    kc = torch.zeros(9, 2, 256, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    full = O.full_attention(x, w, kc, vc, 0, "prefill")
+    kc2 = torch.zeros_like(kc)
+    vc2 = torch.zeros_like(kc)
+    O.full_attention(x[:8], w, kc2, vc2, 0, "prefill")
+    last = O.full_attention(x[8:], w, kc2, vc2, 8, "decode")
+    assert (last.float() - full[8:].float()).abs().max() <= 2e-2
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
