@@ -19,8 +19,11 @@
 //    ds_read_b64_tr_b16.  The P^T operand is the S^T accumulator itself
 //    (same lane mapping), so no shuffles are needed between the two MFMAs.
 //  * the 4 waves merge in LDS; the workgroup writes one (m, l, O) partial.
-//  * decode_gqa_combine merges the partials of all splits, normalises,
-//    optionally applies the sigmoid output gate, and writes bf16.
+//  * decode_gqa_combine merges the partials of all splits with one load
+//    round per thread, normalises, optionally applies the sigmoid output gate
+//    and writes bf16.  (An in-kernel "last workgroup merges" tree was tried:
+//    its device-scope fences write back the XCD's L2 per workgroup and made
+//    the step 3.5x slower.)
 #include "common.h"
 
 namespace q36 {
@@ -29,14 +32,34 @@ namespace {
 constexpr int kDecWaves = 4;
 constexpr int kDecBlock = 32;          // tokens per wave iteration
 constexpr int kVPitch = 544;           // LDS row pitch in bytes (512 + 32)
-constexpr int kDecLds = kDecWaves * kDecBlock * kVPitch;  // 69632 bytes
+constexpr int kVLds = kDecWaves * kDecBlock * kVPitch;   // 69632 bytes
+constexpr int kQPitch = 528;           // LDS row pitch of the Q^T operand
+constexpr int kDecLds = kVLds + 16 * kQPitch;            // 78080 bytes
+
+constexpr unsigned kMaxSplits = 256;
+
+// Workspace carve-up (fp32).
+struct DecodeWs {
+  float* o;            // [2][nsplit][8][256] split partials (unnormalised)
+  float* ml;           // [2][nsplit][8][2]   running max (log2 domain), sum
+};
+
+__device__ __forceinline__ void store_partial(float* o, float* ml,
+                                              const float* acc, float M,
+                                              float L) {
+  *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  if ((threadIdx.x & 31) == 0) {
+    ml[0] = M;
+    ml[1] = L;
+  }
+}
 
 __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     const bf16* __restrict__ q, bf16* __restrict__ k_cache,
     bf16* __restrict__ v_cache, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
-    unsigned split_tokens, unsigned nsplit, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml) {
+    unsigned split_tokens, unsigned nsplit, DecodeWs ws) {
   __shared__ __attribute__((aligned(16))) char lds[kDecLds];
   const int kvh = blockIdx.y;
   const unsigned split = blockIdx.x;
@@ -61,19 +84,6 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     }
   }
 
-  // B operand Q^T: column li = query head (kvh*8 + li) for li < 8, zero
-  // padding otherwise.  Reduction slot (lg, s, e) <-> dim lg*64 + s*8 + e, so
-  // each lane reads one contiguous 128-byte run of q and of every K row.
-  bf16x8 qf[8];
-  if (li < kGroup) {
-    const bf16x8* qp = reinterpret_cast<const bf16x8*>(
-        q + (size_t)(kvh * kGroup + li) * kD + lg * 64);
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = qp[s];
-  } else {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) qf[s] = bf16x8{};
-  }
 
   f32x4 o[16];
 #pragma unroll
@@ -82,10 +92,12 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   const float scale = 0.0625f * kLog2e;
   char* vbuf = lds + wave * kDecBlock * kVPitch;
 
-  for (unsigned t0 = begin + wave * kDecBlock; t0 < end;
-       t0 += kDecWaves * kDecBlock) {
-    // K fragments for two 16-token tiles (A operand rows = tokens).
-    bf16x8 kf[2][8];
+  // Software pipeline: the K fragments and V rows of the next block are
+  // requested as soon as the registers holding the current block are free,
+  // so HBM latency overlaps the softmax and PV work.
+  bf16x8 kf[2][8];
+  uint4 vr[16];
+  auto load_k = [&](unsigned t0) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       const unsigned tok = t0 + tt * 16 + li;
@@ -93,16 +105,17 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
         const bf16* krow = (has_new && tok == position)
                                ? k_new + kvh * kD
                                : k_cache + ((size_t)tok * kHkv + kvh) * kD;
-        const bf16x8* kp = reinterpret_cast<const bf16x8*>(krow + lg * 64);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) kf[tt][s] = kp[s];
+        for (int s = 0; s < 8; ++s)
+          kf[tt][s] = *reinterpret_cast<const bf16x8*>(krow + 32 * s + 8 * lg);
       } else {
 #pragma unroll
         for (int s = 0; s < 8; ++s) kf[tt][s] = bf16x8{};
       }
     }
-    // V rows into registers: row = 2c + lane/32, 16-byte chunk = lane%32.
-    uint4 vr[16];
+  };
+  // V rows: row = 2c + lane/32, 16-byte chunk = lane%32 (fully coalesced).
+  auto load_v = [&](unsigned t0) {
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
       const unsigned tok = t0 + 2 * c + (lane >> 5);
@@ -115,13 +128,45 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
         vr[c] = uint4{0u, 0u, 0u, 0u};
       }
     }
+  };
 
+  const unsigned stride = kDecWaves * kDecBlock;
+  unsigned t0 = begin + wave * kDecBlock;
+  if (t0 < end) {
+    load_k(t0);
+    load_v(t0);
+  }
+
+  // Q staging overlaps the first block's HBM latency.
+  // B operand Q^T: column li = query head (kvh*8 + li) for li < 8, zero
+  // padding otherwise; kept in LDS (rows of kQPitch bytes) and re-read per
+  // block to free registers for the load pipeline.  Reduction step s covers
+  // dims s*32 + 8*lg .. +8, so one K load instruction reads 16 rows x 64
+  // contiguous bytes.
+  char* qs = lds + kVLds;
+  {
+    const int r = threadIdx.x >> 4, c = threadIdx.x & 15;   // 16 rows x 16 chunks
+    uint4 a = uint4{0u, 0u, 0u, 0u}, b = uint4{0u, 0u, 0u, 0u};
+    if (r < kGroup) {
+      const uint4* src = reinterpret_cast<const uint4*>(q + (size_t)(kvh * kGroup + r) * kD);
+      a = src[c];
+      b = src[c + 16];
+    }
+    *reinterpret_cast<uint4*>(qs + r * kQPitch + c * 16) = a;
+    *reinterpret_cast<uint4*>(qs + r * kQPitch + (c + 16) * 16) = b;
+  }
+  __syncthreads();
+  const char* qrow = qs + li * kQPitch + lg * 16;
+  for (; t0 < end; t0 += stride) {
+    const unsigned tn = t0 + stride;
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      s0 = mfma16x16x32(kf[0][s], qf[s], s0);
-      s1 = mfma16x16x32(kf[1][s], qf[s], s1);
+      const bf16x8 qf = *reinterpret_cast<const bf16x8*>(qrow + 64 * s);
+      s0 = mfma16x16x32(kf[0][s], qf, s0);
+      s1 = mfma16x16x32(kf[1][s], qf, s1);
     }
+    if (tn < end) load_k(tn);
     // Lane holds S^T[token t0 + 16*tt + 4*lg + r][head li].
     float sc[8];
 #pragma unroll
@@ -155,6 +200,7 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
       *reinterpret_cast<uint4*>(vbuf + (2 * c + (lane >> 5)) * kVPitch +
                                 (lane & 31) * 16) = vr[c];
     }
+    if (tn < end) load_v(tn);
     bf16x8 pb;
 #pragma unroll
     for (int r = 0; r < 8; ++r) pb[r] = f2bf(p[r]);
@@ -188,9 +234,9 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     }
   }
   __syncthreads();
+  const int h = threadIdx.x >> 5;          // 0..7: head within the group
+  const int d0 = (threadIdx.x & 31) * 8;   // 8 dims per thread
   {
-    const int h = threadIdx.x >> 5;          // 0..7
-    const int d0 = (threadIdx.x & 31) * 8;   // 8 dims per thread
     float mw[kDecWaves], M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) {
@@ -207,14 +253,9 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
       for (int e = 0; e < 8; ++e) acc[e] += f * src[e];
     }
     const size_t slot = ((size_t)kvh * nsplit + split) * kGroup + h;
-    float* dst = ws_o + slot * kD + d0;
-    *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
-    if ((threadIdx.x & 31) == 0) {
-      ws_ml[slot * 2] = M;
-      ws_ml[slot * 2 + 1] = L;
-    }
+    store_partial(ws.o + slot * kD + d0, ws.ml + slot * 2, acc, M, L);
   }
+
 }
 
 // grid = (16 heads, 8 chunks of 32 dims); block = 512 = 32 dims x 16 split
@@ -223,7 +264,7 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
 // groups are merged through LDS.
 constexpr int kCombineGroups = 16;
 constexpr int kCombinePer = 16;
-constexpr unsigned kMaxSplits = kCombineGroups * kCombinePer;  // 256
+static_assert(kCombineGroups * kCombinePer == (int)kMaxSplits, "splits");
 
 __global__ __launch_bounds__(512) void decode_gqa_combine_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
@@ -304,12 +345,15 @@ unsigned choose_split_tokens(unsigned cache_end) {
 
 using namespace q36;
 
+size_t workspace_bytes(unsigned nsplit) {
+  return (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
+}
+
 Q36_EXPORT size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
                                                     unsigned split_tokens) {
   if (cache_end == 0) return 0;
   const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
-  const size_t nsplit = (cache_end + per - 1) / per;
-  return nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
+  return workspace_bytes((cache_end + per - 1) / per);
 }
 
 Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
@@ -318,8 +362,8 @@ Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
                                  unsigned cache_end, unsigned capacity,
                                  const void* gate, unsigned gate_head_stride,
                                  void* out, void* workspace,
-                                 size_t workspace_bytes, unsigned split_tokens,
-                                 void* stream) {
+                                 size_t workspace_bytes_given,
+                                 unsigned split_tokens, void* stream) {
   if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
       out == nullptr || workspace == nullptr || cache_end == 0 ||
       cache_end > capacity || capacity > kMaxTokens ||
@@ -330,19 +374,19 @@ Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
   const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
   const unsigned nsplit = (cache_end + per - 1) / per;
   if (nsplit > kMaxSplits) return Q36_EINVAL;
-  const size_t need = (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
-  if (workspace_bytes < need) return Q36_EINVAL;
+  if (workspace_bytes_given < workspace_bytes(nsplit)) return Q36_EINVAL;
+  DecodeWs ws;
+  ws.o = static_cast<float*>(workspace);
+  ws.ml = ws.o + (size_t)nsplit * kHkv * kGroup * kD;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  float* ws_o = static_cast<float*>(workspace);
-  float* ws_ml = ws_o + (size_t)nsplit * kHkv * kGroup * kD;
   hipLaunchKernelGGL(decode_gqa_split_kernel, dim3(nsplit, kHkv), dim3(256), 0,
                      st, static_cast<const bf16*>(q),
                      static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
                      static_cast<const bf16*>(k_new),
                      static_cast<const bf16*>(v_new), position, cache_end, per,
-                     nsplit, ws_o, ws_ml);
+                     nsplit, ws);
   hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / 32), dim3(512),
-                     0, st, ws_o, ws_ml, nsplit, static_cast<const bf16*>(gate),
+                     0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
                      gate_head_stride, static_cast<bf16*>(out));
   return static_cast<int>(hipGetLastError());
 }

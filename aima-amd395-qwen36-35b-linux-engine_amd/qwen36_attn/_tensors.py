@@ -31,12 +31,13 @@ _SCRATCH: dict[tuple[str, int], torch.Tensor] = {}
 
 
 def scratch(tag: str, nbytes: int, device: torch.device) -> torch.Tensor:
-    """A reusable uint8 device buffer of at least ``nbytes`` bytes.  Calls that
-    share a tag on one device share the buffer, so they are ordered by the
-    stream they run on."""
+    """A reusable, zero-initialised uint8 device buffer of at least ``nbytes``
+    bytes.  Calls that share a tag on one device share the buffer, so they are
+    ordered by the stream they run on (the decode kernel's merge counters rely
+    on the zero fill and leave the buffer zeroed after every call)."""
     key = (tag, device.index if device.index is not None else torch.cuda.current_device())
     buf = _SCRATCH.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _SCRATCH[key] = buf
     return buf

@@ -1,16 +1,18 @@
 """Compile the gfx950 HIP sources into the in-tree C-ABI library.
 
 ``python -m qwen36_attn.build`` (run from the package root) or
-``build_library()`` invokes ``hipcc`` once for all of ``csrc/*.hip`` and
-writes ``qwen36_attn/libqwen36_attn.so``.  Packed-FP32 VALU forms are disabled
-(``-packed-fp32-ops``) for every source.
+``build_library()`` compiles every ``csrc/*.hip`` to an object (in parallel)
+and links ``qwen36_attn/libqwen36_attn.so``.  Packed-FP32 VALU forms are
+disabled (``-packed-fp32-ops``) for every source.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import glob
 import os
 import subprocess
 import sys
+import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG_DIR)
@@ -20,10 +22,17 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
+# Per-source code-generation flags.  The FMHA keeps its output accumulator in
+# VGPRs: with the default AGPR form the conditional rescale makes the compiler
+# copy all 128 accumulator registers AGPR->VGPR on every key tile.
+EXTRA_FLAGS = {
+    "fmha_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
 
 def hip_flags() -> list[str]:
     return [
-        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+        f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
         "-fvisibility=hidden", "-Wall", "-Wno-unused-result",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     ]
@@ -33,23 +42,39 @@ def sources() -> list[str]:
     return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
 
 
+_NOISE = "is not a recognized feature for this target"
+
+
+def _run(cmd: list[str]) -> str:
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(line for line in proc.stderr.splitlines() if _NOISE not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    return err
+
+
 def build_library(verbose: bool = False) -> str:
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    tmp = LIB_PATH + ".tmp"
-    cmd = [HIPCC, *hip_flags(), "-I", CSRC, *srcs, "-o", tmp]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns that it does not know the packed-fp32 feature.
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
-    if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
-    if err.strip() and verbose:
-        print(err, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
+    with tempfile.TemporaryDirectory(prefix="qwen36_build_") as tmpd:
+        jobs = []
+        for src in srcs:
+            obj = os.path.join(tmpd, os.path.basename(src) + ".o")
+            cmd = [HIPCC, *hip_flags(), *EXTRA_FLAGS.get(os.path.basename(src), []),
+                   "-I", CSRC, "-c", src, "-o", obj]
+            jobs.append((cmd, obj))
+        workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
+        with cf.ThreadPoolExecutor(workers) as ex:
+            for (cmd, _), err in zip(jobs, ex.map(lambda j: _run(j[0]), jobs)):
+                if verbose:
+                    print(" ".join(cmd), flush=True)
+                    if err.strip():
+                        print(err, file=sys.stderr)
+        tmp_lib = LIB_PATH + ".tmp"
+        _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
+              *[o for _, o in jobs], "-o", tmp_lib])
+    os.replace(tmp_lib, LIB_PATH)
     return LIB_PATH
 
 

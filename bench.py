@@ -118,7 +118,7 @@ def decode_setup(torch, fa, dev, cache_end, layers, seed):
     lib = fa._lib.load()
     for _ in range(layers):
         nb = lib.qwen36_decode_gqa_workspace_bytes(cache_end, 0)
-        ws.append(torch.empty(nb, dtype=torch.uint8, device=dev))
+        ws.append(torch.zeros(nb, dtype=torch.uint8, device=dev))
 
     def step():
         for i in range(layers):

@@ -59,8 +59,9 @@ int qrt_ck_fmha_q8192_release(void);
  * gate: NULL, or bf16 with gate[h*gate_head_stride + d] the gate of head h
  * (fused q-projection row: stride 512 from its gate half); then
  * out = bf16(bf16(attn) * bf16(sigmoid(gate))) as native_pointwise.hip.cpp
- * :207-222.  out [4096] bf16.  workspace of at least
- * qwen36_decode_gqa_workspace_bytes(cache_end, split_tokens) bytes;
+ * :207-222.  out [4096] bf16.  workspace (split partials) of at least
+ * qwen36_decode_gqa_workspace_bytes(cache_end, split_tokens) bytes; calls
+ * that overlap on one workspace race.
  * split_tokens 0 = automatic, else a multiple of 128 with at most 256 splits. */
 size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
                                          unsigned split_tokens);
