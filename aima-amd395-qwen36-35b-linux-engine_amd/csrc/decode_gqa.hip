@@ -181,12 +181,12 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     mx = wave_max_xor(mx, 16);
     mx = wave_max_xor(mx, 32);
     const float mnew = fmaxf(m, mx);
-    const float alpha = exp2f(m - mnew);
+    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
     float p[8];
     float psum = 0.f;
 #pragma unroll
     for (int r = 0; r < 8; ++r) {
-      p[r] = exp2f(sc[r] - mnew);
+      p[r] = __builtin_amdgcn_exp2f(sc[r] - mnew);
       psum += p[r];
     }
     l = l * alpha + psum;

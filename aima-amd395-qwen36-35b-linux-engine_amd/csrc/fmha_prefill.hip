@@ -11,14 +11,16 @@
 //
 // Kernel plan (MFMA-bound, 16384 flop per unmasked (q,k) pair):
 //  * workgroup = 4 waves = 128 query rows of one head; wave = 32 rows.
-//  * per 64-key tile: K and V are staged in LDS (XOR-swizzled 16-byte chunks,
-//    no padding); S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K from LDS,
-//    B = Q^T held in registers for the whole kernel), online softmax per row
+//  * per 32-key tile: K and V are staged in LDS (padded row-pair blocks, so
+//    every LDS address is a per-lane base plus an immediate); S^T = K Q^T on
+//    v_mfma_f32_32x32x16_bf16 (A = K from LDS, B = Q^T held in registers for
+//    the whole kernel), online softmax per row
 //    in fp32 (exp2 domain), O^T += V^T P^T (A = V^T read with
 //    ds_read_b64_tr_b16, B = P^T taken straight from the S^T accumulator).
 //  * K/V tiles are fetched straight into LDS (global_load_lds_dwordx4, no
-//    register staging) into a double buffer, so the next tile's HBM/L2
-//    latency overlaps the current tile's MFMA work.
+//    register staging) into a double buffer (64 KiB), so the next tile's
+//    HBM/L2 latency overlaps the current tile's MFMA work; two workgroups
+//    (8 waves) share a CU so one wave's softmax overlaps another's MFMAs.
 //  * the O accumulator is rescaled only when a row's running max changes.
 //  * blockIdx -> (KV head, query head, query tile) is XCD-aware: the 8 XCDs
 //    receive workgroups round-robin, so XCDs 0-3 serve KV head 0 and 4-7 KV
@@ -32,20 +34,27 @@ namespace {
 constexpr int kFmWaves = 4;
 constexpr int kFmRowsPerWave = 32;
 constexpr int kFmRows = kFmWaves * kFmRowsPerWave;   // 128
-constexpr int kFmKv = 64;                             // keys per tile
-constexpr int kFmTileBytes = kFmKv * kD * 2;          // 32 KiB
-constexpr int kFmStage = 2 * kFmTileBytes;            // K + V
-constexpr int kFmLds = 2 * kFmStage;                  // double buffered, 128 KiB
-constexpr int kFmLoadsPerWave = kFmTileBytes / 1024 / kFmWaves;  // 8
+constexpr int kFmKv = 32;                             // keys per tile
+constexpr int kRowBytes = kD * 2;                     // 512
+constexpr int kTokBytes = kHkv * kD * 2;              // 1024: one cache row
+// LDS tile layout: block b (0..15) holds key rows b and b+16 back to back
+// (1 KiB, one direct-to-LDS instruction) followed by padding, so that every
+// LDS address below is a per-lane base plus a compile-time offset and both
+// access patterns are bank-conflict-free:
+//  * K blocks are 1040 B apart: 16 rows at one 16-byte column fall in 16
+//    distinct 16-byte bank groups (ds_read_b128 A operand);
+//  * V blocks are 1088 B apart: 8 rows x 64 bytes (ds_read_b64_tr_b16) take
+//    the minimum two passes.
+constexpr int kKBlk = 1040, kVBlk = 1088;
+constexpr int kKTile = 16 * kKBlk;                    // 16640
+constexpr int kVTile = 16 * kVBlk;                    // 17408
+constexpr int kFmStage = kKTile + kVTile;             // 34048
+constexpr int kFmLds = 2 * kFmStage;                  // 68096: double buffer
+constexpr int kFmLoadsPerWave = 16 / kFmWaves;        // 4 blocks per wave
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Physical 16-byte chunk of logical chunk c in row r (XOR swizzles are
-// involutions, so the same map converts physical to logical).
-__device__ __forceinline__ int k_swz(int r, int c) { return c ^ (r & 15); }
-__device__ __forceinline__ int v_swz(int r, int c) { return c ^ ((r & 3) << 2); }
-
-__global__ __launch_bounds__(256, 1) void fmha_prefill_kernel(
+__global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, float* __restrict__ out, unsigned q_tokens,
     unsigned kv_tokens, unsigned n_qtiles) {
@@ -88,47 +97,38 @@ __global__ __launch_bounds__(256, 1) void fmha_prefill_kernel(
   float m = -INFINITY, l = 0.f;
   const float scale = 0.0625f * kLog2e;
 
-  // Direct global->LDS tile fetch through buffer resources (base in SGPRs,
-  // bounds = kv_end rows, so rows past kv_end read as zeros).  Wave
-  // instruction j writes 1 KiB = two 512-byte rows at LDS offset
-  // 1024*(8*wave + j); lane -> (row, physical chunk lane%32) loads the
-  // logical chunk that the swizzle maps there.
-  const int nrec = (int)(kv_end * (unsigned)(kHkv * kD * 2));
+  // Direct global->LDS fetch through buffer resources (base in SGPRs; rows at
+  // or past kv_end are out of bounds and read as zeros).  Wave instruction j
+  // fills block 4*wave + j: lanes 0-31 key row b, lanes 32-63 key row b+16.
+  const int nrec = (int)(kv_end * (unsigned)kTokBytes);
   const __amdgpu_buffer_rsrc_t krs =
       __builtin_amdgcn_make_buffer_rsrc((void*)k, 0, nrec, 0x00020000);
   const __amdgpu_buffer_rsrc_t vrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)v, 0, nrec, 0x00020000);
-  int koff[kFmLoadsPerWave], voff[kFmLoadsPerWave];
-#pragma unroll
-  for (int j = 0; j < kFmLoadsPerWave; ++j) {
-    const int r = 2 * (kFmLoadsPerWave * wave + j) + (lane >> 5);
-    const int p = lane & 31;
-    const int base = r * (kHkv * kD * 2) + kvh * kD * 2;
-    koff[j] = base + k_swz(r, p) * 16;
-    voff[j] = base + v_swz(r, p) * 16;
-  }
+  const int fvoff = (kFmLoadsPerWave * wave + 16 * (lane >> 5)) * kTokBytes +
+                    kvh * kRowBytes + (lane & 31) * 16;
   auto fetch = [&](unsigned kv0, int stage) {
     char* ks = lds + stage * kFmStage;
-    char* vs = ks + kFmTileBytes;
-    const int soff = (int)(kv0 * (unsigned)(kHkv * kD * 2));
+    char* vs = ks + kKTile;
+    const int soff = (int)(kv0 * (unsigned)kTokBytes);
 #pragma unroll
     for (int j = 0; j < kFmLoadsPerWave; ++j) {
       const int blk = kFmLoadsPerWave * wave + j;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(ks + blk * 1024), 16,
-                                               koff[j], soff, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(vs + blk * 1024), 16,
-                                               voff[j], soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(ks + blk * kKBlk), 16,
+                                               fvoff + j * kTokBytes, soff, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(vs + blk * kVBlk), 16,
+                                               fvoff + j * kTokBytes, soff, 0, 0);
     }
   };
 
-  // Per-lane LDS byte offsets of the K (A-operand) and V^T (transposed) reads.
-  const int krow0 = lj * 512;                       // tile half tt adds 32 rows
-  const int kx = lj & 15;
+  // Per-lane LDS bases.  K A operand: key row lj, 16-byte chunk 2*st + lg.
+  const int kbase = (lj & 15) * kKBlk + (lj >> 4) * kRowBytes + lg * 16;
+  // V^T (transposed read): for step st and half h (keys +8), lane reads row
+  // 16*st + 8*h + x, x = 4*lg + (lane%16)/4, 8 bytes at column
+  // 32*((lane/16)&1) + 8*(lane%4) within the 64-byte block of dims dt.
   const int grp = lane >> 4, m16 = lane & 15;
-  const int vrow = 4 * lg + (m16 >> 2);             // + 32tt + 16st (+8)
-  const int vsw = (vrow & 3) << 2;                  // v_swz term (row & 3)
-  const int vcol = 2 * (grp & 1) + ((m16 & 3) >> 1);
-  const int vwb = (m16 & 1) * 8;
+  const int vx = 4 * lg + (m16 >> 2);
+  const int vbase = vx * kVBlk + 32 * (grp & 1) + 8 * (m16 & 3);
 
   const unsigned n_tiles = (kv_end + kFmKv - 1) / kFmKv;
   fetch(0, 0);
@@ -139,87 +139,59 @@ __global__ __launch_bounds__(256, 1) void fmha_prefill_kernel(
     __syncthreads();                 // ... and every wave's; tile t-1 consumed
     if (t + 1 < n_tiles) fetch(kv0 + kFmKv, stage ^ 1);
     if (kv0 > wave_lim) continue;    // every key of the tile is masked for us
-    const char* ks = lds + stage * kFmStage;
-    const char* vs = ks + kFmTileBytes;
+    const char* kp = lds + stage * kFmStage + kbase;
+    const char* vp = lds + stage * kFmStage + kKTile + vbase;
 
-    // S^T[key][row] for two 32-key halves; K fragments are read one step
-    // ahead of the MFMAs that consume them.
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-    bf16x8 ka = *reinterpret_cast<const bf16x8*>(ks + krow0 + ((lg ^ kx) << 4));
-    bf16x8 kb = *reinterpret_cast<const bf16x8*>(ks + 32 * 512 + krow0 + ((lg ^ kx) << 4));
+    // S^T[key][row] for the 32-key tile.
+    f32x16 s0 = f32x16{};
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      bf16x8 na, nb;
-      if (st + 1 < 16) {
-        const int c = ((2 * (st + 1) + lg) ^ kx) << 4;
-        na = *reinterpret_cast<const bf16x8*>(ks + krow0 + c);
-        nb = *reinterpret_cast<const bf16x8*>(ks + 32 * 512 + krow0 + c);
-      }
-      s0 = mfma32x32x16(ka, qf[st], s0);
-      s1 = mfma32x32x16(kb, qf[st], s1);
-      if (st + 1 < 16) {
-        ka = na;
-        kb = nb;
-      }
-    }
-    // Lane holds keys kv0 + 32*tt + 8*(r/4) + 4*lg + r%4 of its row.
+    for (int st = 0; st < 16; ++st)
+      s0 = mfma32x32x16(*reinterpret_cast<const bf16x8*>(kp + st * 32), qf[st], s0);
+    // Lane holds keys kv0 + 8*(r/4) + 4*lg + r%4 of its row.  The running
+    // max m is kept in the scaled log2 domain; since scale > 0 the raw max is
+    // taken first and p = exp2(s*scale - m) is one FMA + one v_exp_f32.
     float mx = -INFINITY;
     const bool diag = kv0 + kFmKv - 1 > wave_first + off || kv0 + kFmKv > kv_tokens;
     if (diag) {  // wave-uniform: only diagonal / ragged tiles pay for masking
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const unsigned key = kv0 + 8 * (r >> 2) + 4 * lg + (r & 3);
-        const bool ok0 = key <= row_lim && key < kv_tokens;
-        const bool ok1 = key + 32 <= row_lim && key + 32 < kv_tokens;
-        s0[r] = ok0 ? s0[r] * scale : -INFINITY;
-        s1[r] = ok1 ? s1[r] * scale : -INFINITY;
-        mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        s0[r] = (key <= row_lim && key < kv_tokens) ? s0[r] : -INFINITY;
+        mx = fmaxf(mx, s0[r]);
       }
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        s0[r] *= scale;
-        s1[r] *= scale;
-        mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[r]);
     }
     mx = wave_max_xor(mx, 32);
-    const float mnew = fmaxf(m, mx);
+    const float mnew = fmaxf(m, mx * scale);
     // Rescale the accumulator only when some row's running max moved.
     if (__any(mnew > m)) {
-      const float alpha = exp2f(m - mnew);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       l *= alpha;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] *= alpha;
     }
     m = mnew;
     float psum = 0.f;
-    bf16x8 pb[2][2];
+    bf16x8 pb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const float p0 = exp2f(s0[r] - mnew);
-      const float p1 = exp2f(s1[r] - mnew);
-      psum += p0 + p1;
-      pb[0][r >> 3][r & 7] = f2bf(p0);
-      pb[1][r >> 3][r & 7] = f2bf(p1);
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale, -mnew));
+      psum += p0;
+      pb[r >> 3][r & 7] = f2bf(p0);
     }
     l += psum;
 
-    // O^T[d][row] += V^T[d][key] P^T[key][row]; step (tt, st) reduction
-    // slots (lg, e) <-> keys 32tt + 16st + 4lg + e and +8 for e >= 4.
+    // O^T[d][row] += V^T[d][key] P^T[key][row]; step st reduction slots
+    // (lg, e) <-> keys 16st + 4lg + e and +8 for e >= 4.
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int st = 0; st < 2; ++st) {
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const char* r0p = vs + (32 * tt + 16 * st + vrow) * 512 + vwb;
-        const char* r1p = r0p + 8 * 512;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          const int c = ((4 * dt + vcol) ^ vsw) << 4;
-          const i16x4 a0 = lds_read_tr16(r0p + c);
-          const i16x4 a1 = lds_read_tr16(r1p + c);
-          o[dt] = mfma32x32x16(cat_bf16x8(a0, a1), pb[tt][st], o[dt]);
-        }
+      for (int dt = 0; dt < 8; ++dt) {
+        const i16x4 a0 = lds_read_tr16(vp + st * kRowBytes + dt * 64);
+        const i16x4 a1 = lds_read_tr16(vp + st * kRowBytes + 8 * kVBlk + dt * 64);
+        o[dt] = mfma32x32x16(cat_bf16x8(a0, a1), pb[st], o[dt]);
       }
     }
   }

@@ -22,12 +22,8 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-# Per-source code-generation flags.  The FMHA keeps its output accumulator in
-# VGPRs: with the default AGPR form the conditional rescale makes the compiler
-# copy all 128 accumulator registers AGPR->VGPR on every key tile.
-EXTRA_FLAGS = {
-    "fmha_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-}
+# Per-source code-generation flags (none needed at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
 
 
 def hip_flags() -> list[str]:
