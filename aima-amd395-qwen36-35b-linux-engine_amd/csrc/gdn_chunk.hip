@@ -3,112 +3,182 @@
 // Restates torch_chunk_gated_delta_rule
 // (benchmarks/shape-lab/four_layer_mini_engine.py:5167-5240); the reference
 // product runs vLLM FLA Triton code objects for this role
-// (native/src/native_linear_prefill.hip.cpp:474-836).  Per v-head h and
-// chunk c of C = 64 tokens (G = in-chunk cumsum of g, q pre-scaled by
-// 1/sqrt(128), q and k l2-normalised):
+// (native/src/native_linear_prefill.hip.cpp:474-836).  Per v-head h and chunk
+// of C = 64 tokens (G = in-chunk cumsum of g; q, k l2-normalised; q scaled by
+// 1/sqrt(128)):
 //   L   = (k*beta) k^T (.) exp(G_i - G_j), strictly lower
-//   T   = (I + L)^-1                       (fle:5207-5211 forward substitution)
+//   T   = (I + L)^-1                     (fle:5207-5211 forward substitution)
 //   U   = T (v*beta),  W = T (k*beta*exp(G))
 //   Aqk = (q k^T) (.) exp(G_i - G_j), lower incl. diagonal
 //   then sequentially over chunks, with the state S [128 k][128 v]:
 //   v' = U - W S;  o = (q*exp(G)) S + Aqk v'
 //   S  = exp(G_last) S + (k*exp(G_last - G))^T v'
 //
+// Arithmetic is fp32-accurate on bf16 matrix cores: every fp32 operand x of a
+// product is split as x = hi + lo (hi = bf16(x), lo = bf16(x - hi)) and
+// x*y ~ hi*hi' + hi*lo' + lo*hi' (relative error ~2^-16), while the raw
+// q/k/v inputs are exact in bf16 and enter single-sided (2 products).  The
+// l2-norm, beta and decay factors are row/column scalings applied in fp32
+// around those products:  k k^T = kinv_i kinv_j (k_raw k_raw^T),
+// W = (T diag(beta e^G kinv)) k_raw,  U = (T diag(beta)) v,
+// Qg S = diag(qinv e^G / sqrt(128)) (q_raw S),
+// Kd^T v' = k_raw^T (diag(kinv e^(G_last - G)) v').
+//
 // Two kernels:
-//  * gdn_chunk_prep  (parallel over chunk x head): everything that does not
-//    depend on S -- U, W, Qg = q*exp(G), Kd = k*exp(G_last-G), Aqk and
-//    exp(G_last) -- written to a workspace.
-//  * gdn_chunk_scan  (grid = 32 heads x 8 blocks of 16 v-columns, sequential
-//    over chunks): the state slice stays in registers for the whole sequence;
-//    each wave owns 32 k-rows of it.
-// All matrix products run on v_mfma_f32_16x16x4_f32 so the arithmetic is
-// fp32 like the reference (no bf16 rounding of derived operands).
+//  * gdn_chunk_prep (grid = chunks x 32 heads): everything independent of S
+//    -- U (fp32), W and Aqk (hi/lo bf16), the two row scales and
+//    exp(G_last) -- into the workspace.  T = (I+L)^-1 is formed blockwise:
+//    16x16 diagonal blocks by forward substitution, off-diagonal blocks by
+//    fp32 MFMA products.
+//  * gdn_chunk_scan (grid = 32 heads x 8 blocks of 16 v-columns,
+//    sequential over chunks): the 128x16 state slice lives in registers in
+//    the MFMA accumulator layout, which is also the B-operand layout of the
+//    next chunk's W S product (the reduction index is permuted to match).
 #include "common.h"
 
 namespace q36 {
 namespace {
 
-constexpr int kC = 64;            // chunk length
-constexpr int kPK = 132;          // LDS pitch (floats) of 64x128 tiles
-constexpr int kPT = 68;           // LDS pitch (floats) of 64x64 tiles
-constexpr int kScanVB = 16;       // v-columns per scan workgroup
+constexpr int kC = 64;
+constexpr int kPitchR = 136;   // bf16 row pitch (272 B) of [64][128] tiles
+constexpr int kPitchT = 72;    // bf16 row pitch (144 B) of transposed tiles
+constexpr int kPitchF = 68;    // fp32 row pitch of [64][64] matrices
+constexpr float kQScale = 0.08838834764831845f;   // 1/sqrt(128)
 
-struct PrepLds {
-  float kn[kC * kPK];   // normalised k
-  float qn[kC * kPK];   // normalised, scaled q
-  float vv[kC * kPK];   // raw v
-  float lt[kC * kPT];   // L, then T in place
-  float aq[kC * kPT];   // Aqk
-  float gs[kC];         // in-chunk cumsum of g
-  float bs[kC];         // beta
+// Workspace: one record per (chunk, head).
+constexpr size_t kOffU = 0;                           // fp32 [64][128]
+constexpr size_t kOffWh = kOffU + 64 * 128 * 4;       // bf16 [64][128]
+constexpr size_t kOffWl = kOffWh + 64 * 128 * 2;
+constexpr size_t kOffAh = kOffWl + 64 * 128 * 2;      // bf16 [64][64]
+constexpr size_t kOffAl = kOffAh + 64 * 64 * 2;
+constexpr size_t kOffRsq = kOffAl + 64 * 64 * 2;      // fp32 [64]
+constexpr size_t kOffRsk = kOffRsq + 256;             // fp32 [64]
+constexpr size_t kOffEgl = kOffRsk + 256;             // fp32 [1]
+constexpr size_t kUnitBytes = kOffEgl + 256;
+static_assert(kUnitBytes % 256 == 0, "unit alignment");
+
+struct Unit {
+  float* U;
+  bf16* Wh;
+  bf16* Wl;
+  bf16* Ah;
+  bf16* Al;
+  float* rsq;
+  float* rsk;
+  float* egl;
 };
+
+__device__ __forceinline__ Unit unit_at(char* ws, size_t unit) {
+  char* b = ws + unit * kUnitBytes;
+  return Unit{reinterpret_cast<float*>(b + kOffU), reinterpret_cast<bf16*>(b + kOffWh),
+              reinterpret_cast<bf16*>(b + kOffWl), reinterpret_cast<bf16*>(b + kOffAh),
+              reinterpret_cast<bf16*>(b + kOffAl), reinterpret_cast<float*>(b + kOffRsq),
+              reinterpret_cast<float*>(b + kOffRsk), reinterpret_cast<float*>(b + kOffEgl)};
+}
+
+__device__ __forceinline__ void split2(float x, bf16& h, bf16& l) {
+  h = f2bf(x);
+  l = f2bf(x - bf2f(h));
+}
 
 __device__ __forceinline__ float rsqrt_rn(float x) {
   return (float)(1.0 / sqrt((double)x));
+}
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// ---------------------------------------------------------------------------
+// Phase A
+// ---------------------------------------------------------------------------
+
+struct PrepLds {
+  // kr, qr and xm are dead once T is complete; the hi/lo T operands alias them.
+  union {
+    struct {
+      bf16 kr[kC * kPitchR];        // k_raw row-major
+      bf16 qr[kC * kPitchR];        // q_raw row-major
+      float xm[kC * kPitchF];       // block-inversion scratch
+    } a;
+    struct {
+      bf16 tuh[kC * kPitchT], tul[kC * kPitchT];   // T diag(beta)
+      bf16 twh[kC * kPitchT], twl[kC * kPitchT];   // T diag(beta e^G kinv)
+    } b;
+  } u;
+  bf16 kt[128 * kPitchT];           // k_raw transposed [d][tok]
+  bf16 vt[128 * kPitchT];           // v transposed [d][tok]
+  float lm[kC * kPitchF];           // L (strictly lower)
+  float tm[kC * kPitchF];           // T
+  float gs[kC], bs[kC], kinv[kC], qinv[kC], sw[kC];
+};
+
+// C = A B for 16x16 fp32 blocks of [64][kPitchF] matrices (v_mfma 16x16x4).
+__device__ __forceinline__ f32x4 mm16(const float* a, int ar, int ac,
+                                      const float* b, int br, int bc, f32x4 acc,
+                                      int li, int kk) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    acc = mfma16x16x4f32(a[(ar + li) * kPitchF + ac + 4 * s + kk],
+                         b[(br + 4 * s + kk) * kPitchF + bc + li], acc);
+  return acc;
 }
 
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
     unsigned v_token_stride, const float* __restrict__ g,
-    const float* __restrict__ beta, unsigned tokens, float* __restrict__ ws_u,
-    float* __restrict__ ws_w, float* __restrict__ ws_qg,
-    float* __restrict__ ws_kd, float* __restrict__ ws_aq,
-    float* __restrict__ ws_egl) {
+    const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PrepLds& s = *reinterpret_cast<PrepLds*>(smem);
   const unsigned c = blockIdx.x;
   const int h = blockIdx.y;
   const int kh = h * (int)qk_heads / kGdnHv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const size_t unit = (size_t)c * kGdnHv + h;
+  const int li = lane & 15, lg = lane >> 4;
+  const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
 
-  // 1. load + l2-normalise rows: thread -> (row tid/4, dims 32*(tid%4)..+32)
+  // S1. rows -> LDS (row-major k, q; transposed k, v); l2 norms.
   {
     const int r = tid >> 2, p = tid & 3;
     const unsigned tok = c * kC + r;
     const bool valid = tok < tokens;
-    float kx[32], qx[32], vx[32];
+    bf16x8 k8[4], q8[4], v8[4];
     if (valid) {
       const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
       const bf16* qp = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
       const bf16* vp = v + (size_t)tok * v_token_stride + h * kGdnDv + 32 * p;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bf16x8 k8 = reinterpret_cast<const bf16x8*>(kp)[i];
-        const bf16x8 q8 = reinterpret_cast<const bf16x8*>(qp)[i];
-        const bf16x8 v8 = reinterpret_cast<const bf16x8*>(vp)[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          kx[8 * i + e] = bf2f(k8[e]);
-          qx[8 * i + e] = bf2f(q8[e]);
-          vx[8 * i + e] = bf2f(v8[e]);
-        }
+        k8[i] = ld8(kp + 8 * i);
+        q8[i] = ld8(qp + 8 * i);
+        v8[i] = ld8(vp + 8 * i);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) kx[i] = qx[i] = vx[i] = 0.f;
+      for (int i = 0; i < 4; ++i) k8[i] = q8[i] = v8[i] = bf16x8{};
     }
     float kss = 0.f, qss = 0.f;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      kss += kx[i] * kx[i];
-      qss += qx[i] * qx[i];
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<bf16x8*>(&s.u.a.kr[r * kPitchR + 32 * p + 8 * i]) = k8[i];
+      *reinterpret_cast<bf16x8*>(&s.u.a.qr[r * kPitchR + 32 * p + 8 * i]) = q8[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float kx = bf2f(k8[i][e]), qx = bf2f(q8[i][e]);
+        kss += kx * kx;
+        qss += qx * qx;
+        s.kt[(32 * p + 8 * i + e) * kPitchT + r] = k8[i][e];
+        s.vt[(32 * p + 8 * i + e) * kPitchT + r] = v8[i][e];
+      }
     }
     kss += __shfl_xor(kss, 1, 64);
     kss += __shfl_xor(kss, 2, 64);
     qss += __shfl_xor(qss, 1, 64);
     qss += __shfl_xor(qss, 2, 64);
-    const float kinv = rsqrt_rn(kss + 1e-6f);
-    const float qinv = rsqrt_rn(qss + 1e-6f);
-    const float qscale = 0.08838834764831845f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      s.kn[r * kPK + 32 * p + i] = kx[i] * kinv;
-      s.qn[r * kPK + 32 * p + i] = (qx[i] * qinv) * qscale;
-      s.vv[r * kPK + 32 * p + i] = vx[i];
-    }
     if (p == 0) {
+      s.kinv[r] = rsqrt_rn(kss + 1e-6f);
+      s.qinv[r] = rsqrt_rn(qss + 1e-6f);
       s.gs[r] = valid ? g[(size_t)tok * kGdnHv + h] : 0.f;
       s.bs[r] = valid ? beta[(size_t)tok * kGdnHv + h] : 0.f;
     }
@@ -120,224 +190,316 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       acc += s.gs[i];
       s.gs[i] = acc;
     }
-    ws_egl[unit] = expf(acc);
+    un.egl[0] = expf(acc);
   }
   __syncthreads();
-
-  // 2. Qg and Kd to the workspace (fp32, [unit][64][128]).
-  {
-    const int r = tid >> 2, p = tid & 3;
+  if (tid < kC) {
+    const int r = tid;
     const float eg = expf(s.gs[r]);
-    const float ed = expf(s.gs[kC - 1] - s.gs[r]);
-    float* qg = ws_qg + (unit * kC + r) * kGdnDk + 32 * p;
-    float* kd = ws_kd + (unit * kC + r) * kGdnDk + 32 * p;
-#pragma unroll
-    for (int i = 0; i < 32; i += 4) {
-      const float* qs = &s.qn[r * kPK + 32 * p + i];
-      const float* ks = &s.kn[r * kPK + 32 * p + i];
-      *reinterpret_cast<f32x4*>(qg + i) =
-          f32x4{qs[0] * eg, qs[1] * eg, qs[2] * eg, qs[3] * eg};
-      *reinterpret_cast<f32x4*>(kd + i) =
-          f32x4{ks[0] * ed, ks[1] * ed, ks[2] * ed, ks[3] * ed};
-    }
+    un.rsq[r] = (s.qinv[r] * kQScale) * eg;
+    un.rsk[r] = s.kinv[r] * expf(s.gs[kC - 1] - s.gs[r]);
+    s.sw[r] = (s.bs[r] * eg) * s.kinv[r];
   }
 
-  // 3. K K^T and Q K^T on the 10 lower 16x16 tiles (20 tile jobs, 5/wave).
-  const int li = lane & 15, kk = lane >> 4;
+  // S3. k k^T and q k^T on the 10 lower 16x16 tiles (bf16 MFMA, exact
+  // products of the raw inputs), then scaled in fp32.
   for (int job = wave; job < 20; job += 4) {
     const bool is_q = job >= 10;
     int t = is_q ? job - 10 : job;
     int rt = 0;
     while (t > rt) { t -= rt + 1; ++rt; }
     const int ct = t;
-    const float* arow = (is_q ? s.qn : s.kn) + (16 * rt + li) * kPK + kk;
-    const float* brow = s.kn + (16 * ct + li) * kPK + kk;
+    const bf16* arow = (is_q ? s.u.a.qr : s.u.a.kr) + (16 * rt + li) * kPitchR + 8 * lg;
+    const bf16* brow = s.u.a.kr + (16 * ct + li) * kPitchR + 8 * lg;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int st = 0; st < kGdnDk / 4; ++st)
-      acc = mfma16x16x4f32(arow[4 * st], brow[4 * st], acc);
-    // acc[r] = dot(row 16rt + 4kk + r, col 16ct + li)
+#pragma unroll
+    for (int st = 0; st < 4; ++st) acc = mfma16x16x32(ld8(arow + 32 * st), ld8(brow + 32 * st), acc);
+    const int j = 16 * ct + li;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int i = 16 * rt + 4 * kk + r, j = 16 * ct + li;
+      const int i = 16 * rt + 4 * lg + r;
       const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
       if (is_q) {
-        s.aq[i * kPT + j] = j <= i ? acc[r] * decay : 0.f;
+        const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc[r]) * decay : 0.f;
+        bf16 ah, al;
+        split2(a, ah, al);
+        un.Ah[i * kC + j] = ah;
+        un.Al[i * kC + j] = al;
       } else {
-        s.lt[i * kPT + j] = j < i ? (acc[r] * s.bs[i]) * decay : 0.f;
+        s.lm[i * kPitchF + j] =
+            j < i ? (((s.kinv[i] * s.kinv[j]) * acc[r]) * s.bs[i]) * decay : 0.f;
       }
     }
   }
-  // zero the strictly-upper 16x16 tiles of both matrices
+  // zero the strictly-upper 16x16 tiles (L, T and the stored Aqk)
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int i = idx >> 6, j = idx & 63;
     if ((j >> 4) > (i >> 4)) {
-      s.lt[i * kPT + j] = 0.f;
-      s.aq[i * kPT + j] = 0.f;
+      s.lm[i * kPitchF + j] = 0.f;
+      s.tm[i * kPitchF + j] = 0.f;
+      un.Ah[idx] = f2bf(0.f);
+      un.Al[idx] = f2bf(0.f);
     }
   }
   __syncthreads();
 
-  // 4. T = (I + L)^-1 by forward substitution, row by row (wave 0, lane = col).
-  if (wave == 0) {
-    const int j = lane;
-    s.lt[0 * kPT + j] = j == 0 ? 1.f : 0.f;
-    for (int i = 1; i < kC; ++i) {
+  // S4. diagonal 16x16 blocks of T = (I + L)^-1: wave b inverts block b,
+  // lane j < 16 owns column j (forward substitution, as fle:5207-5211).
+  if (li == lane) {  // lanes 0..15 of each wave
+    const int b = wave, j = lane;
+    float t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
       float acc = 0.f;
-      // The wave reads all of row i of L before any lane overwrites it: the
-      // lanes run the loop in lockstep and LDS operations of one wave retire
-      // in order.
-      for (int m = 0; m < i; ++m) acc += s.lt[i * kPT + m] * s.lt[m * kPT + j];
-      s.lt[i * kPT + j] = j < i ? -acc : (j == i ? 1.f : 0.f);
+#pragma unroll
+      for (int m = 0; m < i; ++m) acc += s.lm[(16 * b + i) * kPitchF + 16 * b + m] * t[m];
+      t[i] = i == j ? 1.f : (i > j ? -acc : 0.f);
     }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s.tm[(16 * b + i) * kPitchF + 16 * b + j] = t[i];
+  }
+  __syncthreads();
+  // S5. off-diagonal blocks by distance d: T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj.
+  {
+    const int kk = lg;
+    for (int d = 1; d < 4; ++d) {
+      const int bj = wave, bi = wave + d;
+      if (bi < 4) {
+        f32x4 x = {0.f, 0.f, 0.f, 0.f};
+        for (int kb = bj; kb < bi; ++kb)
+          x = mm16(s.lm, 16 * bi, 16 * kb, s.tm, 16 * kb, 16 * bj, x, li, kk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s.u.a.xm[(16 * bi + 4 * kk + r) * kPitchF + 16 * bj + li] = x[r];
+        // same wave reads its own LDS writes back in order
+        f32x4 y = mm16(s.tm, 16 * bi, 16 * bi, s.u.a.xm, 16 * bi, 16 * bj,
+                       f32x4{0.f, 0.f, 0.f, 0.f}, li, kk);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s.tm[(16 * bi + 4 * kk + r) * kPitchF + 16 * bj + li] = -y[r];
+      }
+      __syncthreads();
+    }
+  }
+
+  // S6. hi/lo operands T diag(beta) and T diag(beta e^G kinv) (aliasing kr/qr/xm).
+  for (int idx = tid; idx < kC * kC; idx += 256) {
+    const int i = idx >> 6, m = idx & 63;
+    const float t = s.tm[i * kPitchF + m];
+    bf16 h0, l0, h1, l1;
+    split2(t * s.bs[m], h0, l0);
+    split2(t * s.sw[m], h1, l1);
+    s.u.b.tuh[i * kPitchT + m] = h0;
+    s.u.b.tul[i * kPitchT + m] = l0;
+    s.u.b.twh[i * kPitchT + m] = h1;
+    s.u.b.twl[i * kPitchT + m] = l1;
   }
   __syncthreads();
 
-  // 5. U = T (v*beta), W = T (k*beta*exp(G)); wave w -> column tiles 2w, 2w+1.
+  // S7. U = (T diag beta) v, W = (T diag(beta e^G kinv)) k_raw; wave w takes
+  // the 16-column tiles 2w, 2w+1 of both.  T is lower triangular, so the
+  // second 32-token step is skipped for the first two row tiles.
   for (int ctl = 0; ctl < 2; ++ctl) {
     const int ct = 2 * wave + ctl;
     const int col = 16 * ct + li;
+    const bf16* vb = s.vt + col * kPitchT + 8 * lg;
+    const bf16* kb = s.kt + col * kPitchT + 8 * lg;
     for (int rt = 0; rt < 4; ++rt) {
       f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
-      const int nst = 4 * (rt + 1);   // T is lower triangular
+      const int nst = rt < 2 ? 1 : 2;
       for (int st = 0; st < nst; ++st) {
-        const int m = 4 * st + kk;
-        const float a = s.lt[(16 * rt + li) * kPT + m];
-        const float bm = s.bs[m];
-        const float bu = s.vv[m * kPK + col] * bm;
-        const float bw = s.kn[m * kPK + col] * (bm * expf(s.gs[m]));
-        au = mfma16x16x4f32(a, bu, au);
-        aw = mfma16x16x4f32(a, bw, aw);
+        const int ao = (16 * rt + li) * kPitchT + 32 * st + 8 * lg;
+        const bf16x8 bv = ld8(vb + 32 * st), bk = ld8(kb + 32 * st);
+        au = mfma16x16x32(ld8(s.u.b.tuh + ao), bv, au);
+        au = mfma16x16x32(ld8(s.u.b.tul + ao), bv, au);
+        aw = mfma16x16x32(ld8(s.u.b.twh + ao), bk, aw);
+        aw = mfma16x16x32(ld8(s.u.b.twl + ao), bk, aw);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const size_t o = (unit * kC + 16 * rt + 4 * kk + r) * kGdnDv + col;
-        ws_u[o] = au[r];
-        ws_w[o] = aw[r];
+        const int row = 16 * rt + 4 * lg + r;
+        un.U[row * kGdnDv + col] = au[r];
+        bf16 wh, wl;
+        split2(aw[r], wh, wl);
+        un.Wh[row * kGdnDk + col] = wh;
+        un.Wl[row * kGdnDk + col] = wl;
       }
     }
   }
-  // 6. Aqk to the workspace.
-  for (int idx = tid; idx < kC * kC; idx += 256)
-    ws_aq[unit * kC * kC + idx] = s.aq[(idx >> 6) * kPT + (idx & 63)];
 }
 
-// grid = (32 heads, 8 v-blocks); block = 4 waves; wave w owns k-rows
-// 32w .. 32w+31 of the state slice S[:, v0 .. v0+16).
-__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
-    const float* __restrict__ ws_u, const float* __restrict__ ws_w,
-    const float* __restrict__ ws_qg, const float* __restrict__ ws_kd,
-    const float* __restrict__ ws_aq, const float* __restrict__ ws_egl,
-    const float* state_in, float* state_out, bf16* __restrict__ out,
-    unsigned tokens, unsigned n_chunks) {
-  __shared__ float red_v[4][kC][kScanVB];
-  __shared__ float red_o[4][kC][kScanVB];
-  __shared__ float vp[kC][kScanVB];
-  __shared__ float oq[kC][kScanVB];
-  const int h = blockIdx.x;
-  const int v0 = blockIdx.y * kScanVB;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int li = lane & 15, kk = lane >> 4;
+// ---------------------------------------------------------------------------
+// Phase B
+// ---------------------------------------------------------------------------
 
-  // S in MFMA C-layout: sreg[kt][r] = S[32w + 16kt + 4kk + r][v0 + li].
+constexpr int kVB = 16;   // v-columns per scan workgroup
+
+struct ScanLds {
+  bf16 kt[128 * kPitchT];               // chunk k_raw transposed [k][tok]
+  float red_v[4][kC][kVB];
+  float red_o[4][kC][kVB];
+  float oq[kC][kVB];
+  bf16 vph[kVB * kPitchT], vpl[kVB * kPitchT];   // v'  [v][tok] hi/lo
+  bf16 vqh[kVB * kPitchT], vql[kVB * kPitchT];   // rsk*v' [v][tok] hi/lo
+  float rsq[kC], rsk[kC];
+};
+
+// A operand of the W S / q S products for token row `tok`: reduction slot
+// (lg, e) <-> k = 32*wave + 16*(e/4) + 4*lg + e%4 (the state's register layout).
+__device__ __forceinline__ bf16x8 ld_perm(const bf16* row, int wave, int lg) {
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(row + 32 * wave + 4 * lg);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(row + 32 * wave + 16 + 4 * lg);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+__global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
+    const bf16* __restrict__ q, const bf16* __restrict__ k, unsigned qk_heads,
+    unsigned qk_token_stride, char* __restrict__ ws, const float* state_in,
+    float* state_out, bf16* __restrict__ out, unsigned tokens,
+    unsigned n_chunks) {
+  __shared__ __attribute__((aligned(16))) ScanLds s;
+  const int h = blockIdx.x;
+  const int v0 = blockIdx.y * kVB;
+  const int kh = h * (int)qk_heads / kGdnHv;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int li = lane & 15, lg = lane >> 4;
+
+  // State slice in the MFMA C layout: sreg[t][r] = S[32w + 16t + 4lg + r][v0 + li].
   f32x4 sreg[2];
   const size_t sb = (size_t)h * kGdnDk * kGdnDv + v0 + li;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 32 * wave + 16 * kt + 4 * kk + r;
-      sreg[kt][r] = state_in ? state_in[sb + (size_t)row * kGdnDv] : 0.f;
+      const int row = 32 * wave + 16 * t + 4 * lg + r;
+      sreg[t][r] = state_in ? state_in[sb + (size_t)row * kGdnDv] : 0.f;
     }
 
   for (unsigned c = 0; c < n_chunks; ++c) {
-    const size_t unit = (size_t)c * kGdnHv + h;
-    const float* W = ws_w + unit * kC * kGdnDk;
-    const float* Qg = ws_qg + unit * kC * kGdnDk;
-    const float* Kd = ws_kd + unit * kC * kGdnDk;
-    const float* U = ws_u + unit * kC * kGdnDv;
-    const float* Aq = ws_aq + unit * kC * kC;
-    // a. partial (W S) and (Qg S) over this wave's 32 k-rows.  Reduction
-    //    step (kt, r) <-> k = 32w + 16kt + 4kk + r, matching sreg's layout.
-    f32x4 pv[4], po[4];
+    const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
+    const unsigned tok0 = c * kC;
+    // global operand loads for this chunk
+    bf16x8 kx[4];
+    const int kr_tok = tid >> 2, kr_p = tid & 3;
+    {
+      const unsigned tok = tok0 + kr_tok;
+      const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * kr_p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kx[i] = tok < tokens ? ld8(kp + 8 * i) : bf16x8{};
+    }
+    bf16x8 wh[4], wl[4], qa[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
-      pv[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      po[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int tok = 16 * tt + li;
+      const int row = 16 * tt + li;
+      wh[tt] = ld_perm(un.Wh + row * kGdnDk, wave, lg);
+      wl[tt] = ld_perm(un.Wl + row * kGdnDk, wave, lg);
+      const unsigned tok = tok0 + row;
+      qa[tt] = tok < tokens
+                   ? ld_perm(q + (size_t)tok * qk_token_stride + kh * kGdnDk, wave, lg)
+                   : bf16x8{};
+    }
+    bf16x8 ah[2], al[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int kc = 32 * wave + 16 * kt + 4 * kk;
-        const f32x4 w4 = *reinterpret_cast<const f32x4*>(W + tok * kGdnDk + kc);
-        const f32x4 q4 = *reinterpret_cast<const f32x4*>(Qg + tok * kGdnDk + kc);
+    for (int st = 0; st < 2; ++st) {
+      ah[st] = ld8(un.Ah + (16 * wave + li) * kC + 32 * st + 8 * lg);
+      al[st] = ld8(un.Al + (16 * wave + li) * kC + 32 * st + 8 * lg);
+    }
+    const float egl = un.egl[0];
+
+    __syncthreads();  // previous chunk's readers of kt / vq / oq are done
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          // B operand: lane (li, kk) supplies S[k(step)][v0 + li]; the step's
-          // k for lane group kk is 32w + 16kt + 4kk + r -- exactly sreg[kt][r].
-          pv[tt] = mfma16x16x4f32(w4[r], sreg[kt][r], pv[tt]);
-          po[tt] = mfma16x16x4f32(q4[r], sreg[kt][r], po[tt]);
-        }
-      }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s.kt[(32 * kr_p + 8 * i + e) * kPitchT + kr_tok] = kx[i][e];
+    if (tid < kC) s.rsq[tid] = un.rsq[tid];
+    else if (tid < 2 * kC) s.rsk[tid - kC] = un.rsk[tid - kC];
+
+    // B operand: S hi/lo, slot (lg, e) = sreg[e/4][e%4].
+    bf16x8 sh, sl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bf16 hh, ll;
+      split2(sreg[e >> 2][e & 3], hh, ll);
+      sh[e] = hh;
+      sl[e] = ll;
+    }
+    // partial (W S) and (q_raw S) over this wave's 32 state rows
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      f32x4 pv = {0.f, 0.f, 0.f, 0.f}, po = {0.f, 0.f, 0.f, 0.f};
+      pv = mfma16x16x32(wh[tt], sh, pv);
+      pv = mfma16x16x32(wh[tt], sl, pv);
+      pv = mfma16x16x32(wl[tt], sh, pv);
+      po = mfma16x16x32(qa[tt], sh, po);
+      po = mfma16x16x32(qa[tt], sl, po);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        red_v[wave][16 * tt + 4 * kk + r][li] = pv[tt][r];
-        red_o[wave][16 * tt + 4 * kk + r][li] = po[tt][r];
+        s.red_v[wave][16 * tt + 4 * lg + r][li] = pv[r];
+        s.red_o[wave][16 * tt + 4 * lg + r][li] = po[r];
       }
     }
     __syncthreads();
-    // b. reduce over waves: v' = U - W S; o partial = Qg S.
-    for (int e = tid; e < kC * kScanVB; e += 256) {
-      const int tok = e >> 4, col = e & 15;
-      const float ws = red_v[0][tok][col] + red_v[1][tok][col] +
-                       red_v[2][tok][col] + red_v[3][tok][col];
-      vp[tok][col] = U[tok * kGdnDv + v0 + col] - ws;
-      oq[tok][col] = red_o[0][tok][col] + red_o[1][tok][col] +
-                     red_o[2][tok][col] + red_o[3][tok][col];
+    // reduce over waves: v' = U - W S; o partial = rsq * (q_raw S)
+    {
+      const int tok = tid >> 2, vq = (tid & 3) * 4;
+      const f32x4 u4 = *reinterpret_cast<const f32x4*>(un.U + tok * kGdnDv + v0 + vq);
+      const float rq = s.rsq[tok], rk = s.rsk[tok];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int col = vq + e;
+        const float wsum = s.red_v[0][tok][col] + s.red_v[1][tok][col] +
+                           s.red_v[2][tok][col] + s.red_v[3][tok][col];
+        const float vp = u4[e] - wsum;
+        s.oq[tok][col] = rq * (s.red_o[0][tok][col] + s.red_o[1][tok][col] +
+                               s.red_o[2][tok][col] + s.red_o[3][tok][col]);
+        bf16 a, b;
+        split2(vp, a, b);
+        s.vph[col * kPitchT + tok] = a;
+        s.vpl[col * kPitchT + tok] = b;
+        split2(rk * vp, a, b);
+        s.vqh[col * kPitchT + tok] = a;
+        s.vql[col * kPitchT + tok] = b;
+      }
     }
     __syncthreads();
-    // c. o rows 16w .. 16w+15 = oq + Aqk v'  (Aqk lower triangular).
+    // o rows 16w .. 16w+15 = oq + Aqk v' (Aqk is lower triangular).
     {
       f32x4 acc;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = oq[16 * wave + 4 * kk + r][li];
-      const int nst = 4 * (wave + 1);
+      for (int r = 0; r < 4; ++r) acc[r] = s.oq[16 * wave + 4 * lg + r][li];
+      const int nst = wave < 2 ? 1 : 2;
       for (int st = 0; st < nst; ++st) {
-        const int m = 4 * st + kk;
-        acc = mfma16x16x4f32(Aq[(16 * wave + li) * kC + m], vp[m][li], acc);
+        const bf16x8 bh = ld8(s.vph + li * kPitchT + 32 * st + 8 * lg);
+        const bf16x8 bl = ld8(s.vpl + li * kPitchT + 32 * st + 8 * lg);
+        acc = mfma16x16x32(ah[st], bh, acc);
+        acc = mfma16x16x32(ah[st], bl, acc);
+        acc = mfma16x16x32(al[st], bh, acc);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const unsigned tok = c * kC + 16 * wave + 4 * kk + r;
-        if (tok < tokens)
-          out[((size_t)tok * kGdnHv + h) * kGdnDv + v0 + li] = f2bf(acc[r]);
+        const unsigned tok = tok0 + 16 * wave + 4 * lg + r;
+        if (tok < tokens) out[((size_t)tok * kGdnHv + h) * kGdnDv + v0 + li] = f2bf(acc[r]);
       }
     }
-    // d. S = exp(G_last) S + Kd^T v'.
-    const float egl = ws_egl[unit];
+    // S = exp(G_last) S + k_raw^T (rsk v')
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x4 acc = sreg[kt] * egl;
-      const int krow = 32 * wave + 16 * kt + li;
-#pragma unroll 4
-      for (int st = 0; st < kC / 4; ++st) {
-        const int m = 4 * st + kk;
-        acc = mfma16x16x4f32(Kd[m * kGdnDk + krow], vp[m][li], acc);
+    for (int t = 0; t < 2; ++t) {
+      f32x4 acc = sreg[t] * egl;
+      const int krow = 32 * wave + 16 * t + li;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const bf16x8 a = ld8(s.kt + krow * kPitchT + 32 * st + 8 * lg);
+        acc = mfma16x16x32(a, ld8(s.vqh + li * kPitchT + 32 * st + 8 * lg), acc);
+        acc = mfma16x16x32(a, ld8(s.vql + li * kPitchT + 32 * st + 8 * lg), acc);
       }
-      sreg[kt] = acc;
+      sreg[t] = acc;
     }
   }
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 32 * wave + 16 * kt + 4 * kk + r;
-      state_out[sb + (size_t)row * kGdnDv] = sreg[kt][r];
+      const int row = 32 * wave + 16 * t + 4 * lg + r;
+      state_out[sb + (size_t)row * kGdnDv] = sreg[t][r];
     }
-}
-
-size_t ws_floats(unsigned n_chunks) {
-  const size_t units = (size_t)n_chunks * kGdnHv;
-  return units * (4 * kC * kGdnDk + kC * kC + 1);
 }
 
 }  // namespace
@@ -346,8 +508,8 @@ size_t ws_floats(unsigned n_chunks) {
 using namespace q36;
 
 Q36_EXPORT size_t qwen36_gdn_chunk_prefill_workspace_bytes(unsigned tokens) {
-  const unsigned n_chunks = (tokens + kC - 1) / kC;
-  return ws_floats(n_chunks) * sizeof(float);
+  const size_t n_chunks = (tokens + kC - 1) / kC;
+  return n_chunks * kGdnHv * kUnitBytes;
 }
 
 Q36_EXPORT int qwen36_gdn_chunk_prefill(
@@ -360,18 +522,11 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
       workspace == nullptr || tokens == 0 || tokens > kMaxTokens ||
       (qk_heads != 16u && qk_heads != 32u) ||
       qk_token_stride < qk_heads * kGdnDk ||
-      v_token_stride < (unsigned)(kGdnHv * kGdnDv))
+      v_token_stride < (unsigned)(kGdnHv * kGdnDv) ||
+      (qk_token_stride % 8) != 0 || (v_token_stride % 8) != 0)
     return Q36_EINVAL;
   const unsigned n_chunks = (tokens + kC - 1) / kC;
-  if (workspace_bytes < ws_floats(n_chunks) * sizeof(float)) return Q36_EINVAL;
-  float* base = static_cast<float*>(workspace);
-  const size_t big = (size_t)n_chunks * kGdnHv * kC * kGdnDk;
-  float* ws_u = base;
-  float* ws_w = ws_u + big;
-  float* ws_qg = ws_w + big;
-  float* ws_kd = ws_qg + big;
-  float* ws_aq = ws_kd + big;
-  float* ws_egl = ws_aq + (size_t)n_chunks * kGdnHv * kC * kC;
+  if (workspace_bytes < (size_t)n_chunks * kGdnHv * kUnitBytes) return Q36_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   static bool attr_set = false;
   if (!attr_set) {
@@ -381,16 +536,17 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
     if (e != hipSuccess) return (int)e;
     attr_set = true;
   }
+  char* wsb = static_cast<char*>(workspace);
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256),
                      sizeof(PrepLds), st, static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), static_cast<const bf16*>(v),
                      qk_heads, qk_token_stride, v_token_stride,
                      static_cast<const float*>(g),
-                     static_cast<const float*>(beta), tokens, ws_u, ws_w, ws_qg,
-                     ws_kd, ws_aq, ws_egl);
-  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv, kGdnDv / kScanVB),
-                     dim3(256), 0, st, ws_u, ws_w, ws_qg, ws_kd, ws_aq, ws_egl,
-                     static_cast<const float*>(state_in),
+                     static_cast<const float*>(beta), tokens, wsb);
+  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv, kGdnDv / kVB),
+                     dim3(256), 0, st, static_cast<const bf16*>(q),
+                     static_cast<const bf16*>(k), qk_heads, qk_token_stride,
+                     wsb, static_cast<const float*>(state_in),
                      static_cast<float*>(state_out), static_cast<bf16*>(out),
                      tokens, n_chunks);
   return static_cast<int>(hipGetLastError());
