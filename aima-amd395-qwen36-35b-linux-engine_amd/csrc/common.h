@@ -73,6 +73,17 @@ __device__ __forceinline__ bf16x8 cat_bf16x8(i16x4 lo, i16x4 hi) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS operations
+// (lgkmcnt) but, unlike __syncthreads(), not for its outstanding global loads,
+// so prefetches stay in flight across the barrier.  The signal fences keep
+// the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt(63) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }

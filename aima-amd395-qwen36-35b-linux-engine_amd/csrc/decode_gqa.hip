@@ -10,8 +10,9 @@
 // Layout: k_cache, v_cache are [capacity, 2, 256] bf16 (token stride 512).
 //
 // Kernel plan (HBM-bound, 2048 bytes of K+V per token):
-//  * grid = (nsplit, 2 KV heads); a workgroup owns a contiguous token range
-//    of one KV head; its 4 waves take 32-token blocks round-robin.
+//  * grid = (nsplit, 2 KV heads); the cache's 32-token blocks are dealt to
+//    the splits round-robin (and to the 4 waves of a split in turn), so the
+//    grid sweeps the cache as one contiguous window.
 //  * per block: S^T = K Q^T on MFMA 16x16x32 (A = K streamed from HBM into
 //    registers, B = the 8 query heads of the group, padded to 16 columns),
 //    online softmax per head in fp32 (exp2 domain), then O^T += V^T P^T on
@@ -67,12 +68,17 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;   // MFMA row/column index
   const int lg = lane >> 4;   // 16-lane group
-  const unsigned begin = split * split_tokens;
-  const unsigned end = min(begin + split_tokens, cache_end);
-  // The workgroup whose range holds the new row writes it to the cache (this
+  // 32-token blocks are dealt round-robin: split s owns blocks s, s+nsplit,
+  // ... and its wave w takes every 4th of those.  At any moment the whole
+  // grid therefore reads one contiguous window of the cache (both KV heads of
+  // each row at about the same time), which keeps HBM pages and channels
+  // evenly and sequentially used.
+  const unsigned end = cache_end;
+  (void)split_tokens;
+  // The workgroup that owns the new row's block writes it to the cache (this
   // KV head's half) and reads K/V for that token from k_new/v_new directly,
   // so no other workgroup depends on the write.
-  const bool has_new = k_new != nullptr && position >= begin && position < end;
+  const bool has_new = k_new != nullptr && (position / kDecBlock) % nsplit == split;
   if (has_new && wave == 0) {
     const size_t o = ((size_t)position * kHkv + kvh) * kD;
     if (lane < 32) {
@@ -130,8 +136,8 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     }
   };
 
-  const unsigned stride = kDecWaves * kDecBlock;
-  unsigned t0 = begin + wave * kDecBlock;
+  const unsigned stride = nsplit * kDecWaves * kDecBlock;
+  unsigned t0 = (split + nsplit * wave) * kDecBlock;
   if (t0 < end) {
     load_k(t0);
     load_v(t0);

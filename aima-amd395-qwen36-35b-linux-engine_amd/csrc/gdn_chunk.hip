@@ -29,7 +29,7 @@
 //    -- U (fp32), W and Aqk (hi/lo bf16), the two row scales and
 //    exp(G_last) -- into the workspace.  T = (I+L)^-1 is formed blockwise:
 //    16x16 diagonal blocks by forward substitution, off-diagonal blocks by
-//    fp32 MFMA products.
+//    fp32 MFMA products.  LDS is kept near 72 KB so two workgroups share a CU.
 //  * gdn_chunk_scan (grid = 32 heads x 8 blocks of 16 v-columns,
 //    sequential over chunks): the 128x16 state slice lives in registers in
 //    the MFMA accumulator layout, which is also the B-operand layout of the
@@ -94,22 +94,14 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
 // ---------------------------------------------------------------------------
 
 struct PrepLds {
-  // kr, qr and xm are dead once T is complete; the hi/lo T operands alias them.
+  // k_raw (row-major) is dead once k k^T is in registers; L reuses its space.
   union {
-    struct {
-      bf16 kr[kC * kPitchR];        // k_raw row-major
-      bf16 qr[kC * kPitchR];        // q_raw row-major
-      float xm[kC * kPitchF];       // block-inversion scratch
-    } a;
-    struct {
-      bf16 tuh[kC * kPitchT], tul[kC * kPitchT];   // T diag(beta)
-      bf16 twh[kC * kPitchT], twl[kC * kPitchT];   // T diag(beta e^G kinv)
-    } b;
+    bf16 kr[kC * kPitchR];          // k_raw row-major [tok][d]
+    float lm[kC * kPitchF];         // L (strictly lower)
   } u;
   bf16 kt[128 * kPitchT];           // k_raw transposed [d][tok]
   bf16 vt[128 * kPitchT];           // v transposed [d][tok]
-  float lm[kC * kPitchF];           // L (strictly lower)
-  float tm[kC * kPitchF];           // T
+  float tm[kC * kPitchF];           // T; its upper blocks hold scratch products
   float gs[kC], bs[kC], kinv[kC], qinv[kC], sw[kC];
 };
 
@@ -124,7 +116,26 @@ __device__ __forceinline__ f32x4 mm16(const float* a, int ar, int ac,
   return acc;
 }
 
-__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
+// hi/lo bf16 A operand of row i, columns m0 .. m0+8 of T diag(scale).
+__device__ __forceinline__ void t_operand(const float* tm, const float* scale,
+                                          int i, int m0, bf16x8& hi, bf16x8& lo) {
+  const f32x4 t0 = *reinterpret_cast<const f32x4*>(tm + i * kPitchF + m0);
+  const f32x4 t1 = *reinterpret_cast<const f32x4*>(tm + i * kPitchF + m0 + 4);
+  const f32x4 s0 = *reinterpret_cast<const f32x4*>(scale + m0);
+  const f32x4 s1 = *reinterpret_cast<const f32x4*>(scale + m0 + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    bf16 h, l;
+    split2(t0[e] * s0[e], h, l);
+    hi[e] = h;
+    lo[e] = l;
+    split2(t1[e] * s1[e], h, l);
+    hi[4 + e] = h;
+    lo[4 + e] = l;
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
     unsigned v_token_stride, const float* __restrict__ g,
@@ -136,12 +147,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   const int kh = h * (int)qk_heads / kGdnHv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
+  const unsigned tok0 = c * kC;
   const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
 
-  // S1. rows -> LDS (row-major k, q; transposed k, v); l2 norms.
+  // S1. rows -> LDS (row-major k; transposed k, v); l2 norms of k and q.
   {
     const int r = tid >> 2, p = tid & 3;
-    const unsigned tok = c * kC + r;
+    const unsigned tok = tok0 + r;
     const bool valid = tok < tokens;
     bf16x8 k8[4], q8[4], v8[4];
     if (valid) {
@@ -161,8 +173,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     float kss = 0.f, qss = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<bf16x8*>(&s.u.a.kr[r * kPitchR + 32 * p + 8 * i]) = k8[i];
-      *reinterpret_cast<bf16x8*>(&s.u.a.qr[r * kPitchR + 32 * p + 8 * i]) = q8[i];
+      *reinterpret_cast<bf16x8*>(&s.u.kr[r * kPitchR + 32 * p + 8 * i]) = k8[i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float kx = bf2f(k8[i][e]), qx = bf2f(q8[i][e]);
@@ -192,7 +203,34 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     }
     un.egl[0] = expf(acc);
   }
-  __syncthreads();
+
+  // S2. raw k k^T and q k^T on the 10 lower 16x16 tiles (bf16 MFMA: exact
+  // products of the raw inputs); q fragments come straight from global.
+  f32x4 acc_job[5];
+#pragma unroll
+  for (int jj = 0; jj < 5; ++jj) {
+    const int job = wave + 4 * jj;
+    const bool is_q = job >= 10;
+    int t = is_q ? job - 10 : job;
+    int rt = 0;
+    while (t > rt) { t -= rt + 1; ++rt; }
+    const int ct = t;
+    const bf16* brow = s.u.kr + (16 * ct + li) * kPitchR + 8 * lg;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (is_q) {
+      const unsigned tok = tok0 + 16 * rt + li;
+      const bf16* qrow = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 8 * lg;
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        acc = mfma16x16x32(tok < tokens ? ld8(qrow + 32 * st) : bf16x8{}, ld8(brow + 32 * st), acc);
+    } else {
+      const bf16* arow = s.u.kr + (16 * rt + li) * kPitchR + 8 * lg;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) acc = mfma16x16x32(ld8(arow + 32 * st), ld8(brow + 32 * st), acc);
+    }
+    acc_job[jj] = acc;
+  }
+  __syncthreads();  // k_raw row-major no longer needed; cumsum visible
   if (tid < kC) {
     const int r = tid;
     const float eg = expf(s.gs[r]);
@@ -200,42 +238,36 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     un.rsk[r] = s.kinv[r] * expf(s.gs[kC - 1] - s.gs[r]);
     s.sw[r] = (s.bs[r] * eg) * s.kinv[r];
   }
-
-  // S3. k k^T and q k^T on the 10 lower 16x16 tiles (bf16 MFMA, exact
-  // products of the raw inputs), then scaled in fp32.
-  for (int job = wave; job < 20; job += 4) {
+#pragma unroll
+  for (int jj = 0; jj < 5; ++jj) {
+    const int job = wave + 4 * jj;
     const bool is_q = job >= 10;
     int t = is_q ? job - 10 : job;
     int rt = 0;
     while (t > rt) { t -= rt + 1; ++rt; }
     const int ct = t;
-    const bf16* arow = (is_q ? s.u.a.qr : s.u.a.kr) + (16 * rt + li) * kPitchR + 8 * lg;
-    const bf16* brow = s.u.a.kr + (16 * ct + li) * kPitchR + 8 * lg;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int st = 0; st < 4; ++st) acc = mfma16x16x32(ld8(arow + 32 * st), ld8(brow + 32 * st), acc);
     const int j = 16 * ct + li;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int i = 16 * rt + 4 * lg + r;
       const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
       if (is_q) {
-        const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc[r]) * decay : 0.f;
+        const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
         bf16 ah, al;
         split2(a, ah, al);
         un.Ah[i * kC + j] = ah;
         un.Al[i * kC + j] = al;
       } else {
-        s.lm[i * kPitchF + j] =
-            j < i ? (((s.kinv[i] * s.kinv[j]) * acc[r]) * s.bs[i]) * decay : 0.f;
+        s.u.lm[i * kPitchF + j] =
+            j < i ? (((s.kinv[i] * s.kinv[j]) * acc_job[jj][r]) * s.bs[i]) * decay : 0.f;
       }
     }
   }
-  // zero the strictly-upper 16x16 tiles (L, T and the stored Aqk)
+  // zero the strictly-upper 16x16 tiles of L, T and the stored Aqk
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int i = idx >> 6, j = idx & 63;
     if ((j >> 4) > (i >> 4)) {
-      s.lm[i * kPitchF + j] = 0.f;
+      s.u.lm[i * kPitchF + j] = 0.f;
       s.tm[i * kPitchF + j] = 0.f;
       un.Ah[idx] = f2bf(0.f);
       un.Al[idx] = f2bf(0.f);
@@ -243,82 +275,77 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   }
   __syncthreads();
 
-  // S4. diagonal 16x16 blocks of T = (I + L)^-1: wave b inverts block b,
+  // S3. diagonal 16x16 blocks of T = (I + L)^-1: wave b inverts block b,
   // lane j < 16 owns column j (forward substitution, as fle:5207-5211).
-  if (li == lane) {  // lanes 0..15 of each wave
+  if (li == lane) {
     const int b = wave, j = lane;
     float t[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float acc = 0.f;
 #pragma unroll
-      for (int m = 0; m < i; ++m) acc += s.lm[(16 * b + i) * kPitchF + 16 * b + m] * t[m];
+      for (int m = 0; m < i; ++m) acc += s.u.lm[(16 * b + i) * kPitchF + 16 * b + m] * t[m];
       t[i] = i == j ? 1.f : (i > j ? -acc : 0.f);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) s.tm[(16 * b + i) * kPitchF + 16 * b + j] = t[i];
   }
   __syncthreads();
-  // S5. off-diagonal blocks by distance d: T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj.
-  {
-    const int kk = lg;
-    for (int d = 1; d < 4; ++d) {
-      const int bj = wave, bi = wave + d;
-      if (bi < 4) {
-        f32x4 x = {0.f, 0.f, 0.f, 0.f};
-        for (int kb = bj; kb < bi; ++kb)
-          x = mm16(s.lm, 16 * bi, 16 * kb, s.tm, 16 * kb, 16 * bj, x, li, kk);
+  // S4. off-diagonal blocks by distance d: T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj.
+  // The intermediate sum is parked in the (still zero) upper block (j, i).
+  for (int d = 1; d < 4; ++d) {
+    const int bj = wave, bi = wave + d;
+    if (bi < 4) {
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = bj; kb < bi; ++kb)
+        x = mm16(s.u.lm, 16 * bi, 16 * kb, s.tm, 16 * kb, 16 * bj, x, li, lg);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s.u.a.xm[(16 * bi + 4 * kk + r) * kPitchF + 16 * bj + li] = x[r];
-        // same wave reads its own LDS writes back in order
-        f32x4 y = mm16(s.tm, 16 * bi, 16 * bi, s.u.a.xm, 16 * bi, 16 * bj,
-                       f32x4{0.f, 0.f, 0.f, 0.f}, li, kk);
+      for (int r = 0; r < 4; ++r) s.tm[(16 * bj + 4 * lg + r) * kPitchF + 16 * bi + li] = x[r];
+      // the same wave reads its own LDS writes back in order
+      f32x4 y = mm16(s.tm, 16 * bi, 16 * bi, s.tm, 16 * bj, 16 * bi,
+                     f32x4{0.f, 0.f, 0.f, 0.f}, li, lg);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s.tm[(16 * bi + 4 * kk + r) * kPitchF + 16 * bj + li] = -y[r];
+      for (int r = 0; r < 4; ++r) {
+        s.tm[(16 * bi + 4 * lg + r) * kPitchF + 16 * bj + li] = -y[r];
+        s.tm[(16 * bj + 4 * lg + r) * kPitchF + 16 * bi + li] = 0.f;
       }
-      __syncthreads();
     }
+    __syncthreads();
   }
 
-  // S6. hi/lo operands T diag(beta) and T diag(beta e^G kinv) (aliasing kr/qr/xm).
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    const int i = idx >> 6, m = idx & 63;
-    const float t = s.tm[i * kPitchF + m];
-    bf16 h0, l0, h1, l1;
-    split2(t * s.bs[m], h0, l0);
-    split2(t * s.sw[m], h1, l1);
-    s.u.b.tuh[i * kPitchT + m] = h0;
-    s.u.b.tul[i * kPitchT + m] = l0;
-    s.u.b.twh[i * kPitchT + m] = h1;
-    s.u.b.twl[i * kPitchT + m] = l1;
-  }
-  __syncthreads();
-
-  // S7. U = (T diag beta) v, W = (T diag(beta e^G kinv)) k_raw; wave w takes
-  // the 16-column tiles 2w, 2w+1 of both.  T is lower triangular, so the
-  // second 32-token step is skipped for the first two row tiles.
-  for (int ctl = 0; ctl < 2; ++ctl) {
-    const int ct = 2 * wave + ctl;
-    const int col = 16 * ct + li;
-    const bf16* vb = s.vt + col * kPitchT + 8 * lg;
-    const bf16* kb = s.kt + col * kPitchT + 8 * lg;
-    for (int rt = 0; rt < 4; ++rt) {
-      f32x4 au = {0.f, 0.f, 0.f, 0.f}, aw = {0.f, 0.f, 0.f, 0.f};
-      const int nst = rt < 2 ? 1 : 2;
-      for (int st = 0; st < nst; ++st) {
-        const int ao = (16 * rt + li) * kPitchT + 32 * st + 8 * lg;
-        const bf16x8 bv = ld8(vb + 32 * st), bk = ld8(kb + 32 * st);
-        au = mfma16x16x32(ld8(s.u.b.tuh + ao), bv, au);
-        au = mfma16x16x32(ld8(s.u.b.tul + ao), bv, au);
-        aw = mfma16x16x32(ld8(s.u.b.twh + ao), bk, aw);
-        aw = mfma16x16x32(ld8(s.u.b.twl + ao), bk, aw);
+  // S5. U = (T diag beta) v, W = (T diag(beta e^G kinv)) k_raw; wave w takes
+  // the 16-column tiles 2w, 2w+1 of both.  The hi/lo A operands are formed
+  // on the fly; T is lower triangular, so the second 32-token step is skipped
+  // for the first two row tiles.
+  const int col0 = 32 * wave + li;   // ct = 2w: col0, ct = 2w+1: col0 + 16
+  for (int rt = 0; rt < 4; ++rt) {
+    f32x4 au[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 aw[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    const int nst = rt < 2 ? 1 : 2;
+    for (int st = 0; st < nst; ++st) {
+      bf16x8 tuh, tul, twh, twl;
+      t_operand(s.tm, s.bs, 16 * rt + li, 32 * st + 8 * lg, tuh, tul);
+      t_operand(s.tm, s.sw, 16 * rt + li, 32 * st + 8 * lg, twh, twl);
+#pragma unroll
+      for (int ctl = 0; ctl < 2; ++ctl) {
+        const int col = col0 + 16 * ctl;
+        const bf16x8 bv = ld8(s.vt + col * kPitchT + 32 * st + 8 * lg);
+        const bf16x8 bk = ld8(s.kt + col * kPitchT + 32 * st + 8 * lg);
+        au[ctl] = mfma16x16x32(tuh, bv, au[ctl]);
+        au[ctl] = mfma16x16x32(tul, bv, au[ctl]);
+        aw[ctl] = mfma16x16x32(twh, bk, aw[ctl]);
+        aw[ctl] = mfma16x16x32(twl, bk, aw[ctl]);
       }
+    }
+#pragma unroll
+    for (int ctl = 0; ctl < 2; ++ctl) {
+      const int col = col0 + 16 * ctl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg + r;
-        un.U[row * kGdnDv + col] = au[r];
+        un.U[row * kGdnDv + col] = au[ctl][r];
         bf16 wh, wl;
-        split2(aw[r], wh, wl);
+        split2(aw[ctl][r], wh, wl);
         un.Wh[row * kGdnDk + col] = wh;
         un.Wl[row * kGdnDk + col] = wl;
       }
@@ -373,44 +400,67 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
       sreg[t][r] = state_in ? state_in[sb + (size_t)row * kGdnDv] : 0.f;
     }
 
-  for (unsigned c = 0; c < n_chunks; ++c) {
+  // Operands of one chunk, fetched one chunk ahead (software pipeline): the
+  // loads of chunk c+1 are in flight while chunk c is computed.
+  struct Ops {
+    bf16x8 kx[4];            // k_raw row slice (tok = tid/4, dims 32*(tid%4)..)
+    bf16x8 wh[4], wl[4], qa[4];
+    bf16x8 ah[2], al[2];
+    f32x4 u4;                // U[tok][v0 + 4*(tid%4) ..]
+    float egl, rsq, rsk;     // rsq/rsk of token tid (tid < 64)
+  };
+  const int kr_tok = tid >> 2, kr_p = tid & 3;
+  auto fetch = [&](unsigned c, Ops& o) {
     const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
     const unsigned tok0 = c * kC;
-    // global operand loads for this chunk
-    bf16x8 kx[4];
-    const int kr_tok = tid >> 2, kr_p = tid & 3;
     {
       const unsigned tok = tok0 + kr_tok;
       const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * kr_p;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kx[i] = tok < tokens ? ld8(kp + 8 * i) : bf16x8{};
+      for (int i = 0; i < 4; ++i) o.kx[i] = tok < tokens ? ld8(kp + 8 * i) : bf16x8{};
     }
-    bf16x8 wh[4], wl[4], qa[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       const int row = 16 * tt + li;
-      wh[tt] = ld_perm(un.Wh + row * kGdnDk, wave, lg);
-      wl[tt] = ld_perm(un.Wl + row * kGdnDk, wave, lg);
+      o.wh[tt] = ld_perm(un.Wh + row * kGdnDk, wave, lg);
+      o.wl[tt] = ld_perm(un.Wl + row * kGdnDk, wave, lg);
       const unsigned tok = tok0 + row;
-      qa[tt] = tok < tokens
-                   ? ld_perm(q + (size_t)tok * qk_token_stride + kh * kGdnDk, wave, lg)
-                   : bf16x8{};
+      o.qa[tt] = tok < tokens
+                     ? ld_perm(q + (size_t)tok * qk_token_stride + kh * kGdnDk, wave, lg)
+                     : bf16x8{};
     }
-    bf16x8 ah[2], al[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      ah[st] = ld8(un.Ah + (16 * wave + li) * kC + 32 * st + 8 * lg);
-      al[st] = ld8(un.Al + (16 * wave + li) * kC + 32 * st + 8 * lg);
+      o.ah[st] = ld8(un.Ah + (16 * wave + li) * kC + 32 * st + 8 * lg);
+      o.al[st] = ld8(un.Al + (16 * wave + li) * kC + 32 * st + 8 * lg);
     }
-    const float egl = un.egl[0];
+    o.u4 = *reinterpret_cast<const f32x4*>(un.U + kr_tok * kGdnDv + v0 + 4 * kr_p);
+    o.egl = un.egl[0];
+    o.rsq = tid < kC ? un.rsq[tid] : 0.f;
+    o.rsk = tid < kC ? un.rsk[tid] : 0.f;
+  };
 
-    __syncthreads();  // previous chunk's readers of kt / vq / oq are done
+  // Two operand buffers alternate (loop unrolled by two), so the loads for
+  // chunk c+1 land in registers that chunk c does not read.
+  auto compute = [&](const Ops& o, unsigned c) {
+    const unsigned tok0 = c * kC;
+    const bf16x8* kx = o.kx;
+    const bf16x8* wh = o.wh;
+    const bf16x8* wl = o.wl;
+    const bf16x8* qa = o.qa;
+    const bf16x8* ah = o.ah;
+    const bf16x8* al = o.al;
+    const float egl = o.egl;
+
+    lds_barrier();  // previous chunk's readers of kt / vq / oq are done
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) s.kt[(32 * kr_p + 8 * i + e) * kPitchT + kr_tok] = kx[i][e];
-    if (tid < kC) s.rsq[tid] = un.rsq[tid];
-    else if (tid < 2 * kC) s.rsk[tid - kC] = un.rsk[tid - kC];
+    if (tid < kC) {
+      s.rsq[tid] = o.rsq;
+      s.rsk[tid] = o.rsk;
+    }
 
     // B operand: S hi/lo, slot (lg, e) = sreg[e/4][e%4].
     bf16x8 sh, sl;
@@ -436,11 +486,11 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
         s.red_o[wave][16 * tt + 4 * lg + r][li] = po[r];
       }
     }
-    __syncthreads();
+    lds_barrier();
     // reduce over waves: v' = U - W S; o partial = rsq * (q_raw S)
     {
       const int tok = tid >> 2, vq = (tid & 3) * 4;
-      const f32x4 u4 = *reinterpret_cast<const f32x4*>(un.U + tok * kGdnDv + v0 + vq);
+      const f32x4 u4 = o.u4;
       const float rq = s.rsq[tok], rk = s.rsk[tok];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -459,7 +509,7 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
         s.vql[col * kPitchT + tok] = b;
       }
     }
-    __syncthreads();
+    lds_barrier();
     // o rows 16w .. 16w+15 = oq + Aqk v' (Aqk is lower triangular).
     {
       f32x4 acc;
@@ -491,6 +541,16 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
         acc = mfma16x16x32(a, ld8(s.vql + li * kPitchT + 32 * st + 8 * lg), acc);
       }
       sreg[t] = acc;
+    }
+  };
+  Ops ba, bb;
+  fetch(0, ba);
+  for (unsigned c = 0; c < n_chunks; c += 2) {
+    if (c + 1 < n_chunks) fetch(c + 1, bb);
+    compute(ba, c);
+    if (c + 1 < n_chunks) {
+      if (c + 2 < n_chunks) fetch(c + 2, ba);
+      compute(bb, c + 1);
     }
   }
 #pragma unroll

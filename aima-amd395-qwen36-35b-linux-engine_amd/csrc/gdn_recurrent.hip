@@ -46,6 +46,10 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
   for (unsigned t = 0; t < tokens; ++t) {
     const bf16* qp = q + (size_t)t * qk_token_stride + kh * kGdnDk;
     const bf16* kp = k + (size_t)t * qk_token_stride + kh * kGdnDk;
+    // every per-token input is requested up front (one memory round trip)
+    const float vv = bf2f(v[(size_t)t * v_token_stride + h * kGdnDv + v0 + vi]);
+    const float gt = g[(size_t)t * kGdnHv + h];
+    const float bt = beta[(size_t)t * kGdnHv + h];
     // Full-row sums of squares (every wave computes them redundantly).
     float qa = bf2f(qp[2 * lane]), qb = bf2f(qp[2 * lane + 1]);
     float ka = bf2f(kp[2 * lane]), kb = bf2f(kp[2 * lane + 1]);
@@ -67,8 +71,7 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
         qr[j] = (bf2f(qv8[j]) * qinv) * qscale;
       }
     }
-    const float eg = expf(g[(size_t)t * kGdnHv + h]);
-    const float bt = beta[(size_t)t * kGdnHv + h];
+    const float eg = expf(gt);
     float part = 0.f;
 #pragma unroll
     for (int j = 0; j < kRecRows; ++j) {
@@ -79,10 +82,9 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
     part += __shfl_xor(part, 32, 64);
     const int buf = t & 1;
     if (lane < 16) red[buf][wave][vi] = part;
-    __syncthreads();
+    lds_barrier();
     const float kv = red[buf][0][vi] + red[buf][1][vi] + red[buf][2][vi] +
                      red[buf][3][vi];
-    const float vv = bf2f(v[(size_t)t * v_token_stride + h * kGdnDv + v0 + vi]);
     const float delta = (vv - kv) * bt;
     float op = 0.f;
 #pragma unroll
@@ -92,9 +94,9 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
     }
     op += __shfl_xor(op, 16, 64);
     op += __shfl_xor(op, 32, 64);
-    __syncthreads();  // everyone has read red[buf] for kv
+    lds_barrier();  // everyone has read red[buf] for kv
     if (lane < 16) red[buf][wave][vi] = op;
-    __syncthreads();
+    lds_barrier();
     if (wave == 0 && lane < 16) {
       const float o = red[buf][0][vi] + red[buf][1][vi] + red[buf][2][vi] +
                       red[buf][3][vi];
