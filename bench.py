@@ -44,7 +44,25 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
+    p.add_argument("--only", choices=["decode", "prefill", "gdn", "copy"], default=None,
+                   help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_gqa_128k_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch at S=131072, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (line 'traffic_bytes_per_launch: N')."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
 
 
 def _cpu_info():
@@ -236,6 +254,29 @@ def cpu_baseline(torch, cache_end):
                       f"S={cache_end} (oracle, torch CPU, {_cpu_info()}), x{N_FULL_LAYERS} layers"}
 
 
+def run_only(torch, fa, dev, args):
+    """Single legs for counter runs (rocprofv3 --pmc): the decode headline
+    (10 layers x S=131072, eager launches), the prefill configs, the GDN legs,
+    or a 256 MiB device copy used to calibrate FETCH_SIZE/WRITE_SIZE."""
+    if args.only == "decode":
+        r = bench_decode(torch, fa, dev, 131072, N_FULL_LAYERS, args.steps, args.warmup, False)
+    elif args.only == "prefill":
+        r = [bench_prefill(torch, fa, dev, 8192, 8192, args.steps, args.warmup),
+             bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup)]
+    elif args.only == "gdn":
+        r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
+             bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
+    else:
+        x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        x.fill_(1.0)
+        y = torch.empty_like(x)
+        for _ in range(args.steps):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        r = {"copy_bytes_read": x.numel() * 4, "copy_bytes_written": y.numel() * 4}
+    print(r, file=sys.stderr)
+
+
 def main():
     args = _parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -248,6 +289,9 @@ def main():
     fa._lib.load()
     dev = torch.device("cuda:0")
     use_graph = not args.no_graph
+    if args.only is not None:
+        run_only(torch, fa, dev, args)
+        return
 
     head = bench_decode(torch, fa, dev, 131072, N_FULL_LAYERS, args.steps, args.warmup, use_graph)
     extra = {
@@ -268,7 +312,7 @@ def main():
     alg_bytes = DECODE_BYTES_PER_TOKEN * 131072
     achieved = alg_bytes / (per_layer_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(),
                 "kernel": "qwen36_decode_gqa (write_kv_row + decode_gqa_split + decode_gqa_combine)",
                 "algorithmic_bytes_per_launch": alg_bytes}
     cpu = None if args.no_cpu else cpu_baseline(torch, 131072)
