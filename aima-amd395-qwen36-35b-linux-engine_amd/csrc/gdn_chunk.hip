@@ -30,10 +30,13 @@
 //    exp(G_last) -- into the workspace.  T = (I+L)^-1 is formed blockwise:
 //    16x16 diagonal blocks by forward substitution, off-diagonal blocks by
 //    fp32 MFMA products.  LDS is kept near 72 KB so two workgroups share a CU.
-//  * gdn_chunk_scan (grid = 32 heads x 8 blocks of 16 v-columns,
-//    sequential over chunks): the 128x16 state slice lives in registers in
-//    the MFMA accumulator layout, which is also the B-operand layout of the
-//    next chunk's W S product (the reduction index is permuted to match).
+//  * gdn_chunk_scan (grid = 32 heads x 8 groups of 16 v-columns, sequential
+//    over chunks): wave w owns token tile w of each chunk and state rows
+//    32w .. 32w+31 of its 16 columns, in registers in the MFMA accumulator
+//    layout.  That layout is also the B-operand layout of the next products
+//    (the reduction index -- state row or token -- is permuted to match, and
+//    prep stores the A operands in the same order, fragment-major), so per
+//    chunk only the state tiles and v' (hi/lo bf16) pass through LDS.
 #include "common.h"
 
 namespace q36 {
@@ -45,18 +48,20 @@ constexpr int kPitchT = 72;    // bf16 row pitch (144 B) of transposed tiles
 constexpr int kPitchF = 68;    // fp32 row pitch of [64][64] matrices
 constexpr float kQScale = 0.08838834764831845f;   // 1/sqrt(128)
 
-// Workspace: one record per (chunk, head).
-constexpr size_t kOffU = 0;                           // fp32 [64][128]
-constexpr size_t kOffWh = kOffU + 64 * 128 * 4;       // bf16 [64][128]
+// Workspace: one record per (chunk, head).  The matrices the scan consumes
+// as MFMA A operands are stored fragment-major (frag_off), so each operand
+// is one contiguous 1 KB wave load.
+constexpr size_t kOffU = 0;                           // fp32 [4 tt][8 cg][64 lane][4]
+constexpr size_t kOffWh = kOffU + 64 * 128 * 4;       // bf16 frag [64][128]
 constexpr size_t kOffWl = kOffWh + 64 * 128 * 2;
-constexpr size_t kOffAh = kOffWl + 64 * 128 * 2;      // bf16 [64][64]
+constexpr size_t kOffAh = kOffWl + 64 * 128 * 2;      // bf16 frag [64][64]
 constexpr size_t kOffAl = kOffAh + 64 * 64 * 2;
 constexpr size_t kOffRsq = kOffAl + 64 * 64 * 2;      // fp32 [64]
 constexpr size_t kOffRsk = kOffRsq + 256;             // fp32 [64]
 constexpr size_t kOffEgl = kOffRsk + 256;             // fp32 [1]
-constexpr size_t kUnitBytes = kOffEgl + 256;
-static_assert(kUnitBytes % 256 == 0, "unit alignment");
-
+constexpr size_t kOffKt = kOffEgl + 256;              // bf16 frag [128][64] k_raw^T
+constexpr size_t kOffQ = kOffKt + 128 * 64 * 2;       // bf16 frag [64][128] q_raw
+constexpr size_t kUnitBytes = kOffQ + 64 * 128 * 2;
 struct Unit {
   float* U;
   bf16* Wh;
@@ -66,6 +71,8 @@ struct Unit {
   float* rsq;
   float* rsk;
   float* egl;
+  bf16* kt;
+  bf16* q;
 };
 
 __device__ __forceinline__ Unit unit_at(char* ws, size_t unit) {
@@ -73,7 +80,9 @@ __device__ __forceinline__ Unit unit_at(char* ws, size_t unit) {
   return Unit{reinterpret_cast<float*>(b + kOffU), reinterpret_cast<bf16*>(b + kOffWh),
               reinterpret_cast<bf16*>(b + kOffWl), reinterpret_cast<bf16*>(b + kOffAh),
               reinterpret_cast<bf16*>(b + kOffAl), reinterpret_cast<float*>(b + kOffRsq),
-              reinterpret_cast<float*>(b + kOffRsk), reinterpret_cast<float*>(b + kOffEgl)};
+              reinterpret_cast<float*>(b + kOffRsk), reinterpret_cast<float*>(b + kOffEgl),
+              reinterpret_cast<bf16*>(b + kOffKt),
+              reinterpret_cast<bf16*>(b + kOffQ)};
 }
 
 __device__ __forceinline__ void split2(float x, bf16& h, bf16& l) {
@@ -87,6 +96,16 @@ __device__ __forceinline__ float rsqrt_rn(float x) {
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) {
   return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// Element offset of M[row][col] in the fragment-major layout of a matrix
+// with nkb blocks of 32 reduction columns: [row/16][col/32][lane][8].  Lane
+// 16g + row%16 holds columns 4g..4g+3 and 16+4g..16+4g+3 of its block (the
+// accumulator row order of two stacked 16x16 tiles, which is how the scan's
+// B operands arrive), so an A operand is 16 contiguous bytes per lane.
+__device__ __forceinline__ int frag_off(int row, int col, int nkb) {
+  const int c = col & 31, a = c >> 4, g = (c >> 2) & 3, r = c & 3;
+  return ((((row >> 4) * nkb + (col >> 5)) * 64 + 16 * g + (row & 15)) << 3) + 4 * a + r;
 }
 
 // ---------------------------------------------------------------------------
@@ -183,6 +202,14 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         s.vt[(32 * p + 8 * i + e) * kPitchT + r] = v8[i][e];
       }
     }
+    // q_raw fragments (tile r/16, column block p) for the scan
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const bf16x8 x = q8[g4 >> 1], y = q8[2 + (g4 >> 1)];
+      const int o = 4 * (g4 & 1);
+      *reinterpret_cast<bf16x8*>(un.q + ((((r >> 4) * 4 + p) * 64 + 16 * g4 + (r & 15)) << 3)) =
+          bf16x8{x[o], x[o + 1], x[o + 2], x[o + 3], y[o], y[o + 1], y[o + 2], y[o + 3]};
+    }
     kss += __shfl_xor(kss, 1, 64);
     kss += __shfl_xor(kss, 2, 64);
     qss += __shfl_xor(qss, 1, 64);
@@ -255,8 +282,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
         bf16 ah, al;
         split2(a, ah, al);
-        un.Ah[i * kC + j] = ah;
-        un.Al[i * kC + j] = al;
+        un.Ah[frag_off(i, j, 2)] = ah;
+        un.Al[frag_off(i, j, 2)] = al;
       } else {
         s.u.lm[i * kPitchF + j] =
             j < i ? (((s.kinv[i] * s.kinv[j]) * acc_job[jj][r]) * s.bs[i]) * decay : 0.f;
@@ -269,8 +296,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     if ((j >> 4) > (i >> 4)) {
       s.u.lm[i * kPitchF + j] = 0.f;
       s.tm[i * kPitchF + j] = 0.f;
-      un.Ah[idx] = f2bf(0.f);
-      un.Al[idx] = f2bf(0.f);
+      un.Ah[frag_off(i, j, 2)] = f2bf(0.f);
+      un.Al[frag_off(i, j, 2)] = f2bf(0.f);
     }
   }
   __syncthreads();
@@ -340,16 +367,25 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 #pragma unroll
     for (int ctl = 0; ctl < 2; ++ctl) {
       const int col = col0 + 16 * ctl;
+      reinterpret_cast<f32x4*>(un.U)[(rt * 8 + (col >> 4)) * 64 + 16 * lg + li] = au[ctl];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg + r;
-        un.U[row * kGdnDv + col] = au[ctl][r];
         bf16 wh, wl;
         split2(aw[ctl][r], wh, wl);
-        un.Wh[row * kGdnDk + col] = wh;
-        un.Wl[row * kGdnDk + col] = wl;
+        un.Wh[frag_off(row, col, 4)] = wh;
+        un.Wl[frag_off(row, col, 4)] = wl;
       }
     }
+  }
+  // k_raw^T (fragment-major) for the scan's state update.
+  for (int idx = tid; idx < 128 * 8; idx += 256) {
+    const int row = idx >> 3, ch = idx & 7, t2 = ch >> 2, g4 = ch & 3;
+    const bf16* src = s.kt + row * kPitchT + 32 * t2 + 4 * g4;
+    const bf16x4 a = *reinterpret_cast<const bf16x4*>(src);
+    const bf16x4 b = *reinterpret_cast<const bf16x4*>(src + 16);
+    *reinterpret_cast<bf16x8*>(un.kt + ((((row >> 4) * 2 + t2) * 64 + 16 * g4 + (row & 15)) << 3)) =
+        bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   }
 }
 
@@ -357,209 +393,172 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 // Phase B
 // ---------------------------------------------------------------------------
 
-constexpr int kVB = 16;   // v-columns per scan workgroup
+constexpr int kScanGroups = kGdnDv / 16;   // 16 v-columns per workgroup
 
 struct ScanLds {
-  bf16 kt[128 * kPitchT];               // chunk k_raw transposed [k][tok]
-  float red_v[4][kC][kVB];
-  float red_o[4][kC][kVB];
-  float oq[kC][kVB];
-  bf16 vph[kVB * kPitchT], vpl[kVB * kPitchT];   // v'  [v][tok] hi/lo
-  bf16 vqh[kVB * kPitchT], vql[kVB * kPitchT];   // rsk*v' [v][tok] hi/lo
-  float rsq[kC], rsk[kC];
+  bf16x8 st[8][64];      // [state tile][lane]: S hi (0..3) | lo (4..7)
+  bf16x8 vp[4][64][2];   // [token tile][lane]: {v' hi|lo, rsk v' hi|lo}
 };
 
-// A operand of the W S / q S products for token row `tok`: reduction slot
-// (lg, e) <-> k = 32*wave + 16*(e/4) + 4*lg + e%4 (the state's register layout).
-__device__ __forceinline__ bf16x8 ld_perm(const bf16* row, int wave, int lg) {
-  const bf16x4 a = *reinterpret_cast<const bf16x4*>(row + 32 * wave + 4 * lg);
-  const bf16x4 b = *reinterpret_cast<const bf16x4*>(row + 32 * wave + 16 + 4 * lg);
-  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+__device__ __forceinline__ bf16x8 split4(const f32x4& x) {
+  bf16x8 out;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    bf16 h, l;
+    split2(x[e], h, l);
+    out[e] = h;
+    out[4 + e] = l;
+  }
+  return out;
 }
 
+// B operands (hi, lo) from two published accumulator tiles.
+__device__ __forceinline__ void join_pair(const bf16x8& a, const bf16x8& b,
+                                          bf16x8& hi, bf16x8& lo) {
+  hi = bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  lo = bf16x8{a[4], a[5], a[6], a[7], b[4], b[5], b[6], b[7]};
+}
+
+// grid = 256 workgroups (32 heads x 8 groups of 16 v-columns; the 8 groups
+// of a head share an XCD, so W/q/Aqk/k^T of a chunk are fetched from HBM once
+// per head).  Wave w owns token tile w of every chunk and state tiles 2w,
+// 2w+1 (rows 32w .. 32w+31), in the MFMA accumulator layout:
+//   sreg[i][r] = S[16(2w+i) + 4lg + r][col].
+// Per chunk: every wave publishes its state tiles (hi/lo) to LDS; computes
+// v' and q S for its 16 tokens and publishes v'; then forms its tokens'
+// outputs and updates its state rows.  Operands come straight from global
+// memory in their stored (pre-permuted) order, one chunk ahead.
 __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, unsigned qk_heads,
-    unsigned qk_token_stride, char* __restrict__ ws, const float* state_in,
-    float* state_out, bf16* __restrict__ out, unsigned tokens,
-    unsigned n_chunks) {
-  __shared__ __attribute__((aligned(16))) ScanLds s;
-  const int h = blockIdx.x;
-  const int v0 = blockIdx.y * kVB;
-  const int kh = h * (int)qk_heads / kGdnHv;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const char* __restrict__ ws, const float* state_in, float* state_out,
+    bf16* __restrict__ out, unsigned tokens, unsigned n_chunks) {
+  __shared__ ScanLds s;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  const int h = 4 * xcd + (slot >> 3);
+  const int cg = slot & 7;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
+  const int col = 16 * cg + li;
 
-  // State slice in the MFMA C layout: sreg[t][r] = S[32w + 16t + 4lg + r][v0 + li].
+  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      out, 0, (int)(tokens * kGdnHv * kGdnDv * 2), 0x00020000);
   f32x4 sreg[2];
-  const size_t sb = (size_t)h * kGdnDk * kGdnDv + v0 + li;
+  const size_t sb = (size_t)h * kGdnDk * kGdnDv + col;
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 32 * wave + 16 * t + 4 * lg + r;
-      sreg[t][r] = state_in ? state_in[sb + (size_t)row * kGdnDv] : 0.f;
-    }
+    for (int r = 0; r < 4; ++r)
+      sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
 
-  // Operands of one chunk, fetched one chunk ahead (software pipeline): the
-  // loads of chunk c+1 are in flight while chunk c is computed.
-  struct Ops {
-    bf16x8 kx[4];            // k_raw row slice (tok = tid/4, dims 32*(tid%4)..)
-    bf16x8 wh[4], wl[4], qa[4];
-    bf16x8 ah[2], al[2];
-    f32x4 u4;                // U[tok][v0 + 4*(tid%4) ..]
-    float egl, rsq, rsk;     // rsq/rsk of token tid (tid < 64)
+  struct Stage {
+    bf16x8 wh[4], wl[4], qa[4], ah[2], al[2], kt[2][2];
+    f32x4 u, rsq, rsk;
+    float egl;
   };
-  const int kr_tok = tid >> 2, kr_p = tid & 3;
-  auto fetch = [&](unsigned c, Ops& o) {
-    const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
-    const unsigned tok0 = c * kC;
-    {
-      const unsigned tok = tok0 + kr_tok;
-      const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * kr_p;
+  auto fetch = [&](unsigned c, Stage& st) {
+    const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
+    const bf16x8* Wh = reinterpret_cast<const bf16x8*>(b + kOffWh) + 256 * w + lane;
+    const bf16x8* Wl = reinterpret_cast<const bf16x8*>(b + kOffWl) + 256 * w + lane;
+    const bf16x8* Q = reinterpret_cast<const bf16x8*>(b + kOffQ) + 256 * w + lane;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o.kx[i] = tok < tokens ? ld8(kp + 8 * i) : bf16x8{};
+    for (int k4 = 0; k4 < 4; ++k4) {
+      st.wh[k4] = Wh[64 * k4];
+      st.wl[k4] = Wl[64 * k4];
+      st.qa[k4] = Q[64 * k4];
     }
+    const bf16x8* Ah = reinterpret_cast<const bf16x8*>(b + kOffAh) + 128 * w + lane;
+    const bf16x8* Al = reinterpret_cast<const bf16x8*>(b + kOffAl) + 128 * w + lane;
+    const bf16x8* Kt = reinterpret_cast<const bf16x8*>(b + kOffKt) + 256 * w + lane;
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      const int row = 16 * tt + li;
-      o.wh[tt] = ld_perm(un.Wh + row * kGdnDk, wave, lg);
-      o.wl[tt] = ld_perm(un.Wl + row * kGdnDk, wave, lg);
-      const unsigned tok = tok0 + row;
-      o.qa[tt] = tok < tokens
-                     ? ld_perm(q + (size_t)tok * qk_token_stride + kh * kGdnDk, wave, lg)
-                     : bf16x8{};
+    for (int t2 = 0; t2 < 2; ++t2) {
+      st.ah[t2] = Ah[64 * t2];
+      st.al[t2] = Al[64 * t2];
+      st.kt[0][t2] = Kt[64 * t2];
+      st.kt[1][t2] = Kt[128 + 64 * t2];
     }
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-      o.ah[st] = ld8(un.Ah + (16 * wave + li) * kC + 32 * st + 8 * lg);
-      o.al[st] = ld8(un.Al + (16 * wave + li) * kC + 32 * st + 8 * lg);
-    }
-    o.u4 = *reinterpret_cast<const f32x4*>(un.U + kr_tok * kGdnDv + v0 + 4 * kr_p);
-    o.egl = un.egl[0];
-    o.rsq = tid < kC ? un.rsq[tid] : 0.f;
-    o.rsk = tid < kC ? un.rsk[tid] : 0.f;
+    st.u = reinterpret_cast<const f32x4*>(b + kOffU)[(8 * w + cg) * 64 + lane];
+    st.rsq = *reinterpret_cast<const f32x4*>(b + kOffRsq + 4 * (16 * w + 4 * lg));
+    st.rsk = *reinterpret_cast<const f32x4*>(b + kOffRsk + 4 * (16 * w + 4 * lg));
+    st.egl = *reinterpret_cast<const float*>(b + kOffEgl);
   };
 
-  // Two operand buffers alternate (loop unrolled by two), so the loads for
-  // chunk c+1 land in registers that chunk c does not read.
-  auto compute = [&](const Ops& o, unsigned c) {
-    const unsigned tok0 = c * kC;
-    const bf16x8* kx = o.kx;
-    const bf16x8* wh = o.wh;
-    const bf16x8* wl = o.wl;
-    const bf16x8* qa = o.qa;
-    const bf16x8* ah = o.ah;
-    const bf16x8* al = o.al;
-    const float egl = o.egl;
-
-    lds_barrier();  // previous chunk's readers of kt / vq / oq are done
+  auto step = [&](const Stage& st, unsigned c) {
+    // publish this wave's state tiles
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s.kt[(32 * kr_p + 8 * i + e) * kPitchT + kr_tok] = kx[i][e];
-    if (tid < kC) {
-      s.rsq[tid] = o.rsq;
-      s.rsk[tid] = o.rsk;
-    }
-
-    // B operand: S hi/lo, slot (lg, e) = sreg[e/4][e%4].
-    bf16x8 sh, sl;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      bf16 hh, ll;
-      split2(sreg[e >> 2][e & 3], hh, ll);
-      sh[e] = hh;
-      sl[e] = ll;
-    }
-    // partial (W S) and (q_raw S) over this wave's 32 state rows
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      f32x4 pv = {0.f, 0.f, 0.f, 0.f}, po = {0.f, 0.f, 0.f, 0.f};
-      pv = mfma16x16x32(wh[tt], sh, pv);
-      pv = mfma16x16x32(wh[tt], sl, pv);
-      pv = mfma16x16x32(wl[tt], sh, pv);
-      po = mfma16x16x32(qa[tt], sh, po);
-      po = mfma16x16x32(qa[tt], sl, po);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s.red_v[wave][16 * tt + 4 * lg + r][li] = pv[r];
-        s.red_o[wave][16 * tt + 4 * lg + r][li] = po[r];
-      }
-    }
+    for (int i = 0; i < 2; ++i) s.st[2 * w + i][lane] = split4(sreg[i]);
     lds_barrier();
-    // reduce over waves: v' = U - W S; o partial = rsq * (q_raw S)
-    {
-      const int tok = tid >> 2, vq = (tid & 3) * 4;
-      const f32x4 u4 = o.u4;
-      const float rq = s.rsq[tok], rk = s.rsk[tok];
+    // v' = U - W S and q_raw S for token tile w (reduction over 128 rows)
+    f32x4 aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int col = vq + e;
-        const float wsum = s.red_v[0][tok][col] + s.red_v[1][tok][col] +
-                           s.red_v[2][tok][col] + s.red_v[3][tok][col];
-        const float vp = u4[e] - wsum;
-        s.oq[tok][col] = rq * (s.red_o[0][tok][col] + s.red_o[1][tok][col] +
-                               s.red_o[2][tok][col] + s.red_o[3][tok][col]);
-        bf16 a, b;
-        split2(vp, a, b);
-        s.vph[col * kPitchT + tok] = a;
-        s.vpl[col * kPitchT + tok] = b;
-        split2(rk * vp, a, b);
-        s.vqh[col * kPitchT + tok] = a;
-        s.vql[col * kPitchT + tok] = b;
-      }
+    for (int k4 = 0; k4 < 4; ++k4) {
+      bf16x8 shi, slo;
+      join_pair(s.st[2 * k4][lane], s.st[2 * k4 + 1][lane], shi, slo);
+      aw = mfma16x16x32(st.wh[k4], shi, aw);
+      aq = mfma16x16x32(st.qa[k4], shi, aq);
+      aw = mfma16x16x32(st.wh[k4], slo, aw);
+      aq = mfma16x16x32(st.qa[k4], slo, aq);
+      aw = mfma16x16x32(st.wl[k4], shi, aw);
     }
+    const f32x4 vp = st.u - aw;
+    const f32x4 vz = st.rsk * vp;
+    s.vp[w][lane][0] = split4(vp);
+    s.vp[w][lane][1] = split4(vz);
+    f32x4 acc = st.rsq * aq;
     lds_barrier();
-    // o rows 16w .. 16w+15 = oq + Aqk v' (Aqk is lower triangular).
-    {
-      f32x4 acc;
+    // o = rsq (q_raw S) + Aqk v'  (Aqk is lower triangular: tiles 0, 1 only
+    // need the first 32 tokens)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[r] = s.oq[16 * wave + 4 * lg + r][li];
-      const int nst = wave < 2 ? 1 : 2;
-      for (int st = 0; st < nst; ++st) {
-        const bf16x8 bh = ld8(s.vph + li * kPitchT + 32 * st + 8 * lg);
-        const bf16x8 bl = ld8(s.vpl + li * kPitchT + 32 * st + 8 * lg);
-        acc = mfma16x16x32(ah[st], bh, acc);
-        acc = mfma16x16x32(ah[st], bl, acc);
-        acc = mfma16x16x32(al[st], bh, acc);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const unsigned tok = tok0 + 16 * wave + 4 * lg + r;
-        if (tok < tokens) out[((size_t)tok * kGdnHv + h) * kGdnDv + v0 + li] = f2bf(acc[r]);
-      }
+    for (int t2 = 0; t2 < 2; ++t2) {
+      if (t2 == 1 && w < 2) break;
+      bf16x8 vh, vl;
+      join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
+      acc = mfma16x16x32(st.ah[t2], vh, acc);
+      acc = mfma16x16x32(st.ah[t2], vl, acc);
+      acc = mfma16x16x32(st.al[t2], vh, acc);
     }
     // S = exp(G_last) S + k_raw^T (rsk v')
+    f32x4 sn[2] = {sreg[0] * st.egl, sreg[1] * st.egl};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      f32x4 acc = sreg[t] * egl;
-      const int krow = 32 * wave + 16 * t + li;
+    for (int t2 = 0; t2 < 2; ++t2) {
+      bf16x8 zh, zl;
+      join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const bf16x8 a = ld8(s.kt + krow * kPitchT + 32 * st + 8 * lg);
-        acc = mfma16x16x32(a, ld8(s.vqh + li * kPitchT + 32 * st + 8 * lg), acc);
-        acc = mfma16x16x32(a, ld8(s.vql + li * kPitchT + 32 * st + 8 * lg), acc);
+      for (int i = 0; i < 2; ++i) {
+        sn[i] = mfma16x16x32(st.kt[i][t2], zh, sn[i]);
+        sn[i] = mfma16x16x32(st.kt[i][t2], zl, sn[i]);
       }
-      sreg[t] = acc;
     }
+    sreg[0] = sn[0];
+    sreg[1] = sn[1];
+    // Output rows past the end fall outside the buffer range and are dropped
+    // by the hardware (no branch, so no uncertain store count).
+    const unsigned tb = c * kC + 16 * w + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_buffer_store_b16(
+          __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
+          (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
   };
-  Ops ba, bb;
-  fetch(0, ba);
+
+  // Two operand stages alternate (loop unrolled by two): chunk c+1's loads
+  // are in flight while chunk c is computed.
+  // Two operand stages alternate (loop unrolled by two): chunk c+1's loads
+  // are in flight while chunk c is computed.  Fetches past the last chunk
+  // re-read it, keeping every fetch unconditional.
+  Stage s0, s1;
+  const unsigned last = n_chunks - 1;
+  fetch(0, s0);
   for (unsigned c = 0; c < n_chunks; c += 2) {
-    if (c + 1 < n_chunks) fetch(c + 1, bb);
-    compute(ba, c);
-    if (c + 1 < n_chunks) {
-      if (c + 2 < n_chunks) fetch(c + 2, ba);
-      compute(bb, c + 1);
-    }
+    fetch(c + 1 < last ? c + 1 : last, s1);
+    step(s0, c);
+    if (c + 1 >= n_chunks) break;
+    fetch(c + 2 < last ? c + 2 : last, s0);
+    step(s1, c + 1);
   }
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 32 * wave + 16 * t + 4 * lg + r;
-      state_out[sb + (size_t)row * kGdnDv] = sreg[t][r];
-    }
+    for (int r = 0; r < 4; ++r)
+      state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
 }
 
 }  // namespace
@@ -590,7 +589,7 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   hipStream_t st = static_cast<hipStream_t>(stream);
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(
+    hipError_t e = hipFuncSetAttribute(
         reinterpret_cast<const void*>(gdn_chunk_prep_kernel),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(PrepLds));
     if (e != hipSuccess) return (int)e;
@@ -603,10 +602,9 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
                      qk_heads, qk_token_stride, v_token_stride,
                      static_cast<const float*>(g),
                      static_cast<const float*>(beta), tokens, wsb);
-  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv, kGdnDv / kVB),
-                     dim3(256), 0, st, static_cast<const bf16*>(q),
-                     static_cast<const bf16*>(k), qk_heads, qk_token_stride,
-                     wsb, static_cast<const float*>(state_in),
+  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups),
+                     dim3(256), 0, st, wsb,
+                     static_cast<const float*>(state_in),
                      static_cast<float*>(state_out), static_cast<bf16*>(out),
                      tokens, n_chunks);
   return static_cast<int>(hipGetLastError());
