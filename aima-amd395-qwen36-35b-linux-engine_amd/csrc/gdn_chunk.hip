@@ -248,8 +248,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
       const unsigned tok = tok0 + 16 * rt + li;
       const bf16* qrow = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 8 * lg;
 #pragma unroll
-      for (int st = 0; st < 4; ++st)
-        acc = mfma16x16x32(tok < tokens ? ld8(qrow + 32 * st) : bf16x8{}, ld8(brow + 32 * st), acc);
+      for (int st = 0; st < 4; ++st)   // transposed: D[j][i] = k_j . q_i
+        acc = mfma16x16x32(ld8(brow + 32 * st), tok < tokens ? ld8(qrow + 32 * st) : bf16x8{}, acc);
     } else {
       const bf16* arow = s.u.kr + (16 * rt + li) * kPitchR + 8 * lg;
 #pragma unroll
@@ -273,32 +273,50 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     int rt = 0;
     while (t > rt) { t -= rt + 1; ++rt; }
     const int ct = t;
-    const int j = 16 * ct + li;
+    if (is_q) {
+      // lane holds Aqk[i][j] for i = 16rt + li, j = 16ct + 4lg + r: exactly
+      // half of its A-operand fragment (column block ct/2, half ct%2)
+      const int i = 16 * rt + li;
+      bf16x4 vh, vl;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * rt + 4 * lg + r;
-      const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
-      if (is_q) {
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * ct + 4 * lg + r;
+        const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
         const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
         bf16 ah, al;
         split2(a, ah, al);
-        un.Ah[frag_off(i, j, 2)] = ah;
-        un.Al[frag_off(i, j, 2)] = al;
-      } else {
+        vh[r] = ah;
+        vl[r] = al;
+      }
+      const int o = frag_off(i, 16 * ct + 4 * lg, 2);
+      *reinterpret_cast<bf16x4*>(un.Ah + o) = vh;
+      *reinterpret_cast<bf16x4*>(un.Al + o) = vl;
+    } else {
+      const int j = 16 * ct + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * rt + 4 * lg + r;
+        const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
         s.u.lm[i * kPitchF + j] =
             j < i ? (((s.kinv[i] * s.kinv[j]) * acc_job[jj][r]) * s.bs[i]) * decay : 0.f;
       }
     }
   }
-  // zero the strictly-upper 16x16 tiles of L, T and the stored Aqk
+  // zero the strictly-upper 16x16 tiles of L and T, and of the stored Aqk
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int i = idx >> 6, j = idx & 63;
     if ((j >> 4) > (i >> 4)) {
       s.u.lm[i * kPitchF + j] = 0.f;
       s.tm[i * kPitchF + j] = 0.f;
-      un.Ah[frag_off(i, j, 2)] = f2bf(0.f);
-      un.Al[frag_off(i, j, 2)] = f2bf(0.f);
     }
+  }
+  for (int idx = tid; idx < 6 * 64; idx += 256) {   // 6 upper tiles x 64 lanes
+    const int t = idx >> 6, ln = idx & 63;
+    const int rt = t < 3 ? 0 : (t < 5 ? 1 : 2);
+    const int ct = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+    const int o = frag_off(16 * rt + (ln & 15), 16 * ct + 4 * (ln >> 4), 2);
+    *reinterpret_cast<bf16x4*>(un.Ah + o) = bf16x4{};
+    *reinterpret_cast<bf16x4*>(un.Al + o) = bf16x4{};
   }
   __syncthreads();
 
@@ -360,23 +378,30 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         const bf16x8 bk = ld8(s.kt + col * kPitchT + 32 * st + 8 * lg);
         au[ctl] = mfma16x16x32(tuh, bv, au[ctl]);
         au[ctl] = mfma16x16x32(tul, bv, au[ctl]);
-        aw[ctl] = mfma16x16x32(twh, bk, aw[ctl]);
-        aw[ctl] = mfma16x16x32(twl, bk, aw[ctl]);
+        aw[ctl] = mfma16x16x32(bk, twh, aw[ctl]);   // transposed: W^T
+        aw[ctl] = mfma16x16x32(bk, twl, aw[ctl]);
       }
     }
 #pragma unroll
     for (int ctl = 0; ctl < 2; ++ctl) {
       const int col = col0 + 16 * ctl;
       reinterpret_cast<f32x4*>(un.U)[(rt * 8 + (col >> 4)) * 64 + 16 * lg + li] = au[ctl];
+    }
+    // aw[ctl][r] = W[16rt + li][32w + 16ctl + 4lg + r]: together the whole
+    // A-operand fragment (row tile rt, column block w) of lane 16lg + li
+    bf16x8 wh, wl;
+#pragma unroll
+    for (int ctl = 0; ctl < 2; ++ctl)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * rt + 4 * lg + r;
-        bf16 wh, wl;
-        split2(aw[ctl][r], wh, wl);
-        un.Wh[frag_off(row, col, 4)] = wh;
-        un.Wl[frag_off(row, col, 4)] = wl;
+        bf16 h, l;
+        split2(aw[ctl][r], h, l);
+        wh[4 * ctl + r] = h;
+        wl[4 * ctl + r] = l;
       }
-    }
+    const int fo = ((rt * 4 + wave) * 64 + 16 * lg + li) * 8;
+    *reinterpret_cast<bf16x8*>(un.Wh + fo) = wh;
+    *reinterpret_cast<bf16x8*>(un.Wl + fo) = wl;
   }
   // k_raw^T (fragment-major) for the scan's state update.
   for (int idx = tid; idx < 128 * 8; idx += 256) {
