@@ -22,9 +22,11 @@
 //  * the 4 waves merge in LDS; the workgroup writes one (m, l, O) partial.
 //  * decode_gqa_combine merges the partials of all splits with one load
 //    round per thread, normalises, optionally applies the sigmoid output gate
-//    and writes bf16.  (An in-kernel "last workgroup merges" tree was tried:
-//    its device-scope fences write back the XCD's L2 per workgroup and made
-//    the step 3.5x slower.)
+//    and writes bf16.  Tried and measured slower on MI355X: merging in the
+//    split kernel (a "last workgroup merges" tree or a grid barrier: device-
+//    scope fences write back/invalidate the whole L2, and workgroups polling
+//    a counter slow the stream), and dynamic tail balancing through global
+//    ticket counters (atomic latency and contention exceed the tail saved).
 #include "common.h"
 
 namespace q36 {
@@ -38,6 +40,10 @@ constexpr int kQPitch = 528;           // LDS row pitch of the Q^T operand
 constexpr int kDecLds = kVLds + 16 * kQPitch;            // 78080 bytes
 
 constexpr unsigned kMaxSplits = 256;
+// Default split count: 128 splits x 2 KV heads = one workgroup per CU.
+// (Measured on MI355X at 128K: 128 splits beat 256 -- two workgroups per CU
+// -- and 64..192; one workgroup holding both KV heads was no faster.)
+constexpr unsigned kTargetSplits = 128;
 
 // Workspace carve-up (fp32).
 struct DecodeWs {
@@ -264,81 +270,89 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
 
 }
 
-// grid = (16 heads, 8 chunks of 32 dims); block = 512 = 32 dims x 16 split
-// groups.  Every thread issues all of its partial loads before using any
-// (up to kCombinePer splits), merges them online in registers, and the 16
-// groups are merged through LDS.
-constexpr int kCombineGroups = 16;
-constexpr int kCombinePer = 16;
-static_assert(kCombineGroups * kCombinePer == (int)kMaxSplits, "splits");
+// grid = (16 heads, 16 chunks of 16 dims); block = 256.  Thread t reads the
+// (m, l) of split t and, as (split group t/4, dim quad t%4), the float4
+// partials of splits t/4 + 64u (u < 4): every load is issued up front (one
+// memory round trip).  The split weights 2^(m - M) go through LDS; the
+// weighted partials are reduced over the wave's 16 split groups with
+// shuffles and over the 4 waves through LDS.
+constexpr int kCombineDims = 16;
+static_assert(kMaxSplits == 256, "one (m, l) per combine thread");
 
-__global__ __launch_bounds__(512) void decode_gqa_combine_kernel(
+__global__ __launch_bounds__(256) void decode_gqa_combine_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     unsigned nsplit, const bf16* __restrict__ gate, unsigned gate_head_stride,
     bf16* __restrict__ out) {
-  __shared__ float part_m[kCombineGroups][32];
-  __shared__ float part_a[kCombineGroups][32];
-  __shared__ float part_l[kCombineGroups][32];
+  __shared__ float fw[kMaxSplits];
+  __shared__ float wred[2][4];
+  __shared__ f32x4 part[4][4];
   const int head = blockIdx.x;
   const int kvh = head / kGroup, hh = head % kGroup;
-  const int dsub = threadIdx.x & 31, sg = threadIdx.x >> 5;
-  const int d = blockIdx.y * 32 + dsub;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int dq = tid & 3, sgp = tid >> 2;
+  const int d0 = blockIdx.y * kCombineDims + 4 * dq;
   const size_t base = (size_t)kvh * nsplit * kGroup + hh;  // slot of split 0
 
-  float ms[kCombinePer], os[kCombinePer], ls[kCombinePer];
+  float2 ml = float2{-INFINITY, 0.f};
+  if ((unsigned)tid < nsplit)
+    ml = *reinterpret_cast<const float2*>(ws_ml + (base + (size_t)tid * kGroup) * 2);
+  f32x4 os[4];
 #pragma unroll
-  for (int u = 0; u < kCombinePer; ++u) {
-    const unsigned sp = sg + kCombineGroups * u;
-    const size_t slot = base + (size_t)sp * kGroup;
-    const bool ok = sp < nsplit;
-    ms[u] = ok ? ws_ml[slot * 2] : -INFINITY;
-    ls[u] = ok ? ws_ml[slot * 2 + 1] : 0.f;
-    os[u] = ok ? ws_o[slot * kD + d] : 0.f;
+  for (int u = 0; u < 4; ++u) {
+    const unsigned sp = sgp + 64 * u;
+    os[u] = sp < nsplit
+                ? *reinterpret_cast<const f32x4*>(ws_o + (base + (size_t)sp * kGroup) * kD + d0)
+                : f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float M = -INFINITY;
-#pragma unroll
-  for (int u = 0; u < kCombinePer; ++u) M = fmaxf(M, ms[u]);
-  float acc = 0.f, L = 0.f;
-  if (M != -INFINITY) {
-#pragma unroll
-    for (int u = 0; u < kCombinePer; ++u) {
-      const float f = exp2f(ms[u] - M);  // 0 for empty splits (ms = -inf)
-      acc += f * os[u];
-      L += f * ls[u];
-    }
-  }
-  part_m[sg][dsub] = M;
-  part_a[sg][dsub] = acc;
-  part_l[sg][dsub] = L;
+  float mx = wave_max_xor(ml.x, 1);
+  mx = wave_max_xor(mx, 2);
+  mx = wave_max_xor(mx, 4);
+  mx = wave_max_xor(mx, 8);
+  mx = wave_max_xor(mx, 16);
+  mx = wave_max_xor(mx, 32);
+  if (lane == 0) wred[0][wave] = mx;
   __syncthreads();
-  if (sg == 0) {
-    float Mg = -INFINITY;
+  const float M = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
+  const float f = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
+  fw[tid] = f;
+  float lsum = f * ml.y;
 #pragma unroll
-    for (int i = 0; i < kCombineGroups; ++i) Mg = fmaxf(Mg, part_m[i][dsub]);
-    float a = 0.f, Lg = 0.f;
+  for (int o = 1; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
+  if (lane == 0) wred[1][wave] = lsum;
+  __syncthreads();
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kCombineGroups; ++i) {
-      const float mi = part_m[i][dsub];
-      const float f = mi == -INFINITY ? 0.f : exp2f(mi - Mg);
-      a += f * part_a[i][dsub];
-      Lg += f * part_l[i][dsub];
+  for (int u = 0; u < 4; ++u) acc += fw[(sgp + 64 * u) & (kMaxSplits - 1)] * os[u];
+#pragma unroll
+  for (int o = 4; o < 64; o <<= 1)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
+  if (lane < 4) part[wave][dq] = acc;
+  __syncthreads();
+  if (tid < 4) {
+    const float L = (wred[1][0] + wred[1][1]) + (wred[1][2] + wred[1][3]);
+    const f32x4 a = (part[0][dq] + part[1][dq]) + (part[2][dq] + part[3][dq]);
+    bf16x4 ob;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bf16 x = f2bf(a[e] / L);
+      if (gate != nullptr) {
+        // Reference gate numerics (native_pointwise.hip.cpp:207-222): sigmoid
+        // in fp32, rounded to bf16, product rounded to bf16.
+        const float gv = bf2f(gate[(size_t)head * gate_head_stride + d0 + e]);
+        const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv)));
+        x = f2bf(bf2f(x) * bf2f(sg_b));
+      }
+      ob[e] = x;
     }
-    bf16 ob = f2bf(a / Lg);
-    if (gate != nullptr) {
-      // Reference gate numerics (native_pointwise.hip.cpp:207-222): sigmoid in
-      // fp32, rounded to bf16, product rounded to bf16.
-      const float gv = bf2f(gate[(size_t)head * gate_head_stride + d]);
-      const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv)));
-      ob = f2bf(bf2f(ob) * bf2f(sg_b));
-    }
-    out[head * kD + d] = ob;
+    *reinterpret_cast<bf16x4*>(out + head * kD + d0) = ob;
   }
 }
 
 unsigned choose_split_tokens(unsigned cache_end) {
-  // Aim for ~2 workgroups per CU-slot (256 CUs) on both KV heads while
-  // keeping at least one 32-token block per wave.
-  const unsigned target_splits = kMaxSplits;
+  // Aim for one workgroup per CU (256 CUs) over both KV heads while keeping
+  // at least one 32-token block per wave.
+  const unsigned target_splits = kTargetSplits;
   unsigned per = (cache_end + target_splits - 1) / target_splits;
   const unsigned quantum = kDecWaves * kDecBlock;  // 128
   per = (per + quantum - 1) / quantum * quantum;
@@ -391,7 +405,7 @@ Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
                      static_cast<const bf16*>(k_new),
                      static_cast<const bf16*>(v_new), position, cache_end, per,
                      nsplit, ws);
-  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / 32), dim3(512),
+  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / kCombineDims), dim3(256),
                      0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
                      gate_head_stride, static_cast<bf16*>(out));
   return static_cast<int>(hipGetLastError());

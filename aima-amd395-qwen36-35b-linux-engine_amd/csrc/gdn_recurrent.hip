@@ -10,9 +10,13 @@
 //   S <- S + k (x) delta;  o = S^T q
 // State layout [32][128 (k)][128 (v)] fp32, as the torch oracle keeps it.
 //
-// HBM-bound (2 MiB read + 2 MiB write per layer step).  grid = 32 heads x 8
-// column blocks of 16 v; a thread owns 8 rows x 1 column of S in registers,
-// so S is read once and written once however many tokens are processed, and
+// HBM-bound (2 MiB read + 2 MiB write per layer step).  Both reductions of
+// a token are done in one round: with kv_old = S^T k and sq_old = S^T q,
+//   kv = e^g kv_old,  delta = (v - kv) beta,  o = e^g sq_old + delta (k.q)
+// (o = S'^T q expanded), so a token costs one cross-wave exchange.
+// grid = 32 heads x 8 blocks of 16 v-columns; thread (rg, cq) owns rows
+// 2rg, 2rg+1 and columns 4cq .. 4cq+3 of its block as two float4, so S is
+// read once and written once however many tokens are processed, and
 // state_in may alias state_out.
 #include "common.h"
 
@@ -20,7 +24,6 @@ namespace q36 {
 namespace {
 
 constexpr int kRecVBlock = 16;
-constexpr int kRecRows = 8;   // k rows per thread: 16 groups x 8 = 128
 
 __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
@@ -28,84 +31,83 @@ __global__ __launch_bounds__(256) void gdn_recurrent_kernel(
     unsigned v_token_stride, const float* __restrict__ g,
     const float* __restrict__ beta, const float* state_in, float* state_out,
     bf16* __restrict__ out, unsigned tokens) {
-  __shared__ float red[2][4][kRecVBlock];
+  __shared__ f32x4 red[2][4][2][4];   // [parity][wave][kv | sq][col quad]
   const int h = blockIdx.x;
   const int v0 = blockIdx.y * kRecVBlock;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int vi = lane & 15;
-  const int kq = wave * 4 + (lane >> 4);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int cq = tid & 3, rg = tid >> 2;
+  const int r0 = 2 * rg;
   const int kh = h * (int)qk_heads / kGdnHv;
-  const size_t sbase = (size_t)h * kGdnDk * kGdnDv + v0 + vi;
+  const size_t sbase = (size_t)h * kGdnDk * kGdnDv + v0 + 4 * cq;
 
-  float s[kRecRows];
-#pragma unroll
-  for (int j = 0; j < kRecRows; ++j)
-    s[j] = state_in[sbase + (size_t)(kq * kRecRows + j) * kGdnDv];
+  f32x4 s0 = *reinterpret_cast<const f32x4*>(state_in + sbase + (size_t)r0 * kGdnDv);
+  f32x4 s1 = *reinterpret_cast<const f32x4*>(state_in + sbase + (size_t)(r0 + 1) * kGdnDv);
 
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
   for (unsigned t = 0; t < tokens; ++t) {
     const bf16* qp = q + (size_t)t * qk_token_stride + kh * kGdnDk;
     const bf16* kp = k + (size_t)t * qk_token_stride + kh * kGdnDk;
     // every per-token input is requested up front (one memory round trip)
-    const float vv = bf2f(v[(size_t)t * v_token_stride + h * kGdnDv + v0 + vi]);
+    const bf16x4 v4 = *reinterpret_cast<const bf16x4*>(
+        v + (size_t)t * v_token_stride + h * kGdnDv + v0 + 4 * cq);
     const float gt = g[(size_t)t * kGdnHv + h];
     const float bt = beta[(size_t)t * kGdnHv + h];
-    // Full-row sums of squares (every wave computes them redundantly).
-    float qa = bf2f(qp[2 * lane]), qb = bf2f(qp[2 * lane + 1]);
-    float ka = bf2f(kp[2 * lane]), kb = bf2f(kp[2 * lane + 1]);
-    float qss = qa * qa + qb * qb, kss = ka * ka + kb * kb;
+    const float qa = bf2f(qp[2 * lane]), qb = bf2f(qp[2 * lane + 1]);
+    const float ka = bf2f(kp[2 * lane]), kb = bf2f(kp[2 * lane + 1]);
+    const float k0 = bf2f(kp[r0]), k1 = bf2f(kp[r0 + 1]);
+    const float q0 = bf2f(qp[r0]), q1 = bf2f(qp[r0 + 1]);
+    // partial S^T k and S^T q over this thread's two rows (raw q, k)
+    f32x4 pk = s0 * k0 + s1 * k1;
+    f32x4 pq = s0 * q0 + s1 * q1;
+    // full-row sums (every wave computes them redundantly)
+    float qss = qa * qa + qb * qb, kss = ka * ka + kb * kb, kq = qa * ka + qb * kb;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       qss += __shfl_xor(qss, o, 64);
       kss += __shfl_xor(kss, o, 64);
+      kq += __shfl_xor(kq, o, 64);
     }
+    // reduce the partials over the wave's 16 row groups (lanes with equal cq)
+#pragma unroll
+    for (int o = 4; o < 64; o <<= 1)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pk[e] += __shfl_xor(pk[e], o, 64);
+        pq[e] += __shfl_xor(pq[e], o, 64);
+      }
+    const int par = t & 1;
+    if (lane < 4) {
+      red[par][wave][0][cq] = pk;
+      red[par][wave][1][cq] = pq;
+    }
+    lds_barrier();
+    const f32x4 kv_raw = red[par][0][0][cq] + red[par][1][0][cq] + red[par][2][0][cq] +
+                         red[par][3][0][cq];
+    const f32x4 sq_raw = red[par][0][1][cq] + red[par][1][1][cq] + red[par][2][1][cq] +
+                         red[par][3][1][cq];
     const float qinv = 1.0f / sqrtf(qss + 1e-6f);
     const float kinv = 1.0f / sqrtf(kss + 1e-6f);
-    float kr[kRecRows], qr[kRecRows];
-    {
-      const bf16x8 kv8 = *reinterpret_cast<const bf16x8*>(kp + kq * kRecRows);
-      const bf16x8 qv8 = *reinterpret_cast<const bf16x8*>(qp + kq * kRecRows);
-#pragma unroll
-      for (int j = 0; j < kRecRows; ++j) {
-        kr[j] = bf2f(kv8[j]) * kinv;
-        qr[j] = (bf2f(qv8[j]) * qinv) * qscale;
-      }
-    }
+    const float qn = qinv * qscale;
     const float eg = expf(gt);
-    float part = 0.f;
+    const float kqn = (kq * kinv) * qn;
+    f32x4 delta, o;
 #pragma unroll
-    for (int j = 0; j < kRecRows; ++j) {
-      s[j] *= eg;
-      part += s[j] * kr[j];
+    for (int e = 0; e < 4; ++e) {
+      const float kv = eg * (kv_raw[e] * kinv);
+      delta[e] = (bf2f(v4[e]) - kv) * bt;
+      o[e] = eg * (sq_raw[e] * qn) + delta[e] * kqn;
     }
-    part += __shfl_xor(part, 16, 64);
-    part += __shfl_xor(part, 32, 64);
-    const int buf = t & 1;
-    if (lane < 16) red[buf][wave][vi] = part;
-    lds_barrier();
-    const float kv = red[buf][0][vi] + red[buf][1][vi] + red[buf][2][vi] +
-                     red[buf][3][vi];
-    const float delta = (vv - kv) * bt;
-    float op = 0.f;
+    s0 = s0 * eg + delta * (k0 * kinv);
+    s1 = s1 * eg + delta * (k1 * kinv);
+    if (rg == 0) {
+      bf16x4 ob;
 #pragma unroll
-    for (int j = 0; j < kRecRows; ++j) {
-      s[j] += kr[j] * delta;
-      op += s[j] * qr[j];
-    }
-    op += __shfl_xor(op, 16, 64);
-    op += __shfl_xor(op, 32, 64);
-    lds_barrier();  // everyone has read red[buf] for kv
-    if (lane < 16) red[buf][wave][vi] = op;
-    lds_barrier();
-    if (wave == 0 && lane < 16) {
-      const float o = red[buf][0][vi] + red[buf][1][vi] + red[buf][2][vi] +
-                      red[buf][3][vi];
-      out[((size_t)t * kGdnHv + h) * kGdnDv + v0 + vi] = f2bf(o);
+      for (int e = 0; e < 4; ++e) ob[e] = f2bf(o[e]);
+      *reinterpret_cast<bf16x4*>(out + ((size_t)t * kGdnHv + h) * kGdnDv + v0 + 4 * cq) = ob;
     }
   }
-#pragma unroll
-  for (int j = 0; j < kRecRows; ++j)
-    state_out[sbase + (size_t)(kq * kRecRows + j) * kGdnDv] = s[j];
+  *reinterpret_cast<f32x4*>(state_out + sbase + (size_t)r0 * kGdnDv) = s0;
+  *reinterpret_cast<f32x4*>(state_out + sbase + (size_t)(r0 + 1) * kGdnDv) = s1;
 }
 
 }  // namespace
@@ -124,7 +126,10 @@ Q36_EXPORT int qwen36_gdn_recurrent(const void* q, const void* k, const void* v,
       out == nullptr || tokens == 0 || tokens > kMaxTokens ||
       (qk_heads != 16u && qk_heads != 32u) ||
       qk_token_stride < qk_heads * kGdnDk ||
-      v_token_stride < (unsigned)(kGdnHv * kGdnDv))
+      v_token_stride < (unsigned)(kGdnHv * kGdnDv) || (v_token_stride % 4) != 0 ||
+      (reinterpret_cast<uintptr_t>(v) % 8) != 0 || (reinterpret_cast<uintptr_t>(out) % 8) != 0 ||
+      (reinterpret_cast<uintptr_t>(state_in) % 16) != 0 ||
+      (reinterpret_cast<uintptr_t>(state_out) % 16) != 0)
     return Q36_EINVAL;
   hipLaunchKernelGGL(gdn_recurrent_kernel, dim3(kGdnHv, kGdnDv / kRecVBlock),
                      dim3(256), 0, static_cast<hipStream_t>(stream),

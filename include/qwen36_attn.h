@@ -111,7 +111,8 @@ int qwen36_output_gate(const void* attn, int attn_is_f32, const void* q_gate,
  *   bf16 raw (l2-normalised in-kernel) with token stride qk_token_stride,
  *   v [T,32,128] with token stride v_token_stride, g/beta [T,32] fp32,
  *   state [32,128(k),128(v)] fp32 (state_out may alias state_in),
- *   out [T,32,128] bf16.
+ *   out [T,32,128] bf16.  v_token_stride % 4 == 0; v and out 8-byte and
+ *   the states 16-byte aligned.
  * qwen36_gdn_chunk_prefill: replaces torch_chunk_gated_delta_rule
  *   (:5167-5240, chunk 64) / the FLA chunk pipeline launched by
  *   native_linear_prefill.hip.cpp:474-836.  Same tensors as the recurrent
