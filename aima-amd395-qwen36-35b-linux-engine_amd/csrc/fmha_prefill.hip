@@ -21,7 +21,8 @@
 //    register staging) into a double buffer (64 KiB), so the next tile's
 //    HBM/L2 latency overlaps the current tile's MFMA work; two workgroups
 //    (8 waves) share a CU so one wave's softmax overlaps another's MFMAs.
-//  * the O accumulator is rescaled only when a row's running max changes.
+//  * the O accumulator is rescaled only when a row's tile max exceeds its
+//    reference max by more than 8 (log2 units), i.e. a few times per row.
 //  * blockIdx -> (KV head, query head, query tile) is XCD-aware: the 8 XCDs
 //    receive workgroups round-robin, so XCDs 0-3 serve KV head 0 and 4-7 KV
 //    head 1 (their L2s then hold one head's K/V), and every XCD issues its
@@ -164,15 +165,20 @@ __global__ __launch_bounds__(256, 2) void fmha_prefill_kernel(
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[r]);
     }
     mx = wave_max_xor(mx, 32);
-    const float mnew = fmaxf(m, mx * scale);
-    // Rescale the accumulator only when some row's running max moved.
-    if (__any(mnew > m)) {
+    // The reference max m may lag the true running max by up to 8 (log2
+    // units): p = 2^(s*scale - m) then stays <= 256, exact enough in fp32
+    // and bf16, and O and l (which share m) are rescaled only when some
+    // row's tile max exceeds its m by more than that -- a few times per row.
+    const float mt = mx * scale;
+    if (__any(mt > m + 8.0f)) {
+      const float mnew = fmaxf(m, mt);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       l *= alpha;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] *= alpha;
+      m = mnew;
     }
-    m = mnew;
+    const float mnew = m;
     float psum = 0.f;
     bf16x8 pb[2];
 #pragma unroll
