@@ -19,6 +19,10 @@ ROOT = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(ROOT, "csrc")
 LIB_NAME = "libqwen36_attn.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# Host-only C++ caller of the FMHA provider ABI (dlopen, like the engine).
+HARNESS_SRC = os.path.join(ROOT, "harness", "provider_harness.cpp")
+HARNESS_PATH = os.path.join(PKG_DIR, "provider_harness")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
@@ -71,7 +75,22 @@ def build_library(verbose: bool = False) -> str:
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
               *[o for _, o in jobs], "-o", tmp_lib])
     os.replace(tmp_lib, LIB_PATH)
+    build_harness(verbose)
     return LIB_PATH
+
+
+def build_harness(verbose: bool = False) -> str:
+    """Compile the provider harness (plain host C++ against the HIP runtime;
+    it loads the library with dlopen, so it does not link it)."""
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           "-I", os.path.join(ROCM, "include"), HARNESS_SRC, "-o", HARNESS_PATH + ".tmp",
+           "-L", os.path.join(ROCM, "lib"), "-lamdhip64", "-ldl",
+           f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    _run(cmd)
+    os.replace(HARNESS_PATH + ".tmp", HARNESS_PATH)
+    return HARNESS_PATH
 
 
 if __name__ == "__main__":
