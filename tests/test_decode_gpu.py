@@ -73,6 +73,28 @@ def test_decode_split_invariance(gpu, split_tokens):
     assert (base - alt).abs().max().item() <= 2e-3
 
 
+@pytest.mark.parametrize("cache_end", [131072, 262143])
+def test_decode_full_size_matches_oracle(gpu, cache_end):
+    """The benchmarked KV lengths (config 5), with the new row appended at the
+    last position, against the oracle's grouped bf16 decode."""
+    from qwen36_attn.full_attention import decode_gqa
+    q, k, v = _inputs(cache_end, seed=cache_end % 1000)
+    g = torch.Generator().manual_seed(7)
+    k_new = torch.randn(2, 256, generator=g).to(torch.bfloat16)
+    v_new = torch.randn(2, 256, generator=g).to(torch.bfloat16)
+    print(f"decode full size cache_end={cache_end}", flush=True)
+    kd, vd = k.to(gpu), v.to(gpu)
+    out = decode_gqa(q.to(gpu), kd, vd, cache_end - 1, cache_end,
+                     k_new=k_new.to(gpu), v_new=v_new.to(gpu))
+    torch.cuda.synchronize()
+    O.write_kv_cache(k, v, k_new.view(1, 2, 256), v_new.view(1, 2, 256), cache_end - 1)
+    assert torch.equal(kd[cache_end - 1].cpu(), k[cache_end - 1])
+    ref = O.decode_attention_grouped_bf16(q.view(1, 16, 256), k, v, cache_end).float()
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max().item() <= TOL_BF16
+
+
 def test_decode_rejects_bad_geometry(gpu):
     from qwen36_attn.full_attention import decode_gqa
     q, k, v = _inputs(64, seed=1)

@@ -52,6 +52,21 @@ def test_prefill_config3_sampled_rows(gpu):
     assert torch.isfinite(got).all()
 
 
+def test_prefill_8k_causal_sampled_rows(gpu):
+    """The benchmarked 8192-token causal prefill: rows spread over the whole
+    range (tile and workgroup edges) against the oracle for those rows."""
+    from qwen36_attn.full_attention import fmha_prefill
+    t = 8192
+    q, k, v = _inputs(t, t, seed=8)
+    print("prefill 8k causal", flush=True)
+    got = fmha_prefill(q.to(gpu), k.to(gpu), v.to(gpu)).cpu()
+    for r in [0, 1, 31, 32, 127, 128, 255, 256, 1000, 4095, 4096, 8063, 8064, 8191]:
+        ref = O.prefill_attention(q[r:r + 1], k[:r + 1], v[:r + 1], position_start=r,
+                                  out_dtype=torch.float32)
+        assert (got[r:r + 1] - ref).abs().max().item() <= TOL_TIGHT, r
+    assert torch.isfinite(got).all()
+
+
 def test_prefix_extension_equals_tail_of_full_prefill(gpu):
     """Bottom-right prefill over S equals the last T rows of a full causal
     prefill over S (prefix-cache continuation)."""
