@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // requested as soon as the registers holding the current block are free,
   // so HBM latency overlaps the softmax and PV work.
   bf16x8 kf[2][8];
-  uint4 vr[16];
+  u32x4 vr[16];
   auto load_k = [&](unsigned t0) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
@@ -119,7 +119,9 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
                                : k_cache + ((size_t)tok * kHkv + kvh) * kD;
 #pragma unroll
         for (int s = 0; s < 8; ++s)
-          kf[tt][s] = *reinterpret_cast<const bf16x8*>(krow + 32 * s + 8 * lg);
+          kf[tt][s] = __builtin_bit_cast(
+              bf16x8, __builtin_nontemporal_load(
+                          reinterpret_cast<const u32x4*>(krow + 32 * s + 8 * lg)));
       } else {
 #pragma unroll
         for (int s = 0; s < 8; ++s) kf[tt][s] = bf16x8{};
@@ -135,9 +137,10 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
         const bf16* vrow = (has_new && tok == position)
                                ? v_new + kvh * kD
                                : v_cache + ((size_t)tok * kHkv + kvh) * kD;
-        vr[c] = *reinterpret_cast<const uint4*>(vrow + (lane & 31) * 8);
+        vr[c] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(vrow + (lane & 31) * 8));
       } else {
-        vr[c] = uint4{0u, 0u, 0u, 0u};
+        vr[c] = u32x4{0u, 0u, 0u, 0u};
       }
     }
   };
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     // Stage V (row-major, padded pitch) in this wave's private LDS slot.
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
-      *reinterpret_cast<uint4*>(vbuf + (2 * c + (lane >> 5)) * kVPitch +
+      *reinterpret_cast<u32x4*>(vbuf + (2 * c + (lane >> 5)) * kVPitch +
                                 (lane & 31) * 16) = vr[c];
     }
     if (tn < end) load_v(tn);
