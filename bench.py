@@ -84,11 +84,20 @@ class Timer:
     def __init__(self, torch):
         self.torch = torch
 
-    def time(self, fn, iters, warmup=2):
+    def time(self, fn, iters, warmup=2, warm_seconds=0.2):
+        """Mean ms per call over `iters` calls, after `warmup` calls and at
+        least `warm_seconds` of back-to-back calls: an idle MI355X runs at a
+        low clock for the first few milliseconds of work, which would
+        otherwise be charged to the timed region."""
         torch = self.torch
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
+        t_end = time.perf_counter() + warm_seconds
+        while time.perf_counter() < t_end:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
         s = torch.cuda.current_stream()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
