@@ -24,8 +24,9 @@
 //    register staging) into a double buffer (64 KiB), so the next tile's
 //    HBM/L2 latency overlaps the current tile's MFMA work; the two waves
 //    on each SIMD let one wave's softmax overlap the other's MFMAs.
-//  * the O accumulator is rescaled only when a row's tile max exceeds its
-//    reference max by more than 8 (log2 units), i.e. a few times per row.
+//  * no per-tile row max: the reference max is the first tile's, raised
+//    (with a rescale of O) only when a tile's probabilities would exceed
+//    2^20, which the per-lane probability sum detects.
 //  * blockIdx -> (KV head, query head, query tile) is XCD-aware: the 8 XCDs
 //    receive workgroups round-robin, so XCDs 0-3 serve KV head 0 and 4-7 KV
 //    head 1 (their L2s then hold one head's K/V), and every XCD issues its
@@ -151,44 +152,52 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
 #pragma unroll
     for (int st = 0; st < 16; ++st)
       s0 = mfma32x32x16(*reinterpret_cast<const bf16x8*>(kp + st * 32), qf[st], s0);
-    // Lane holds keys kv0 + 8*(r/4) + 4*lg + r%4 of its row.  The running
-    // max m is kept in the scaled log2 domain; since scale > 0 the raw max is
-    // taken first and p = exp2(s*scale - m) is one FMA + one v_exp_f32.
-    float mx = -INFINITY;
+    // Lane holds keys kv0 + 8*(r/4) + 4*lg + r%4 of its row.
     const bool diag = kv0 + kFmKv - 1 > wave_first + off || kv0 + kFmKv > kv_tokens;
     if (diag) {  // wave-uniform: only diagonal / ragged tiles pay for masking
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const unsigned key = kv0 + 8 * (r >> 2) + 4 * lg + (r & 3);
         s0[r] = (key <= row_lim && key < kv_tokens) ? s0[r] : -INFINITY;
-        mx = fmaxf(mx, s0[r]);
       }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s0[r]);
     }
-    mx = wave_max_xor(mx, 32);
-    // The reference max m may lag the true running max by up to 8 (log2
-    // units): p = 2^(s*scale - m) then stays <= 256, exact enough in fp32
-    // and bf16, and O and l (which share m) are rescaled only when some
-    // row's tile max exceeds its m by more than that -- a few times per row.
-    const float mt = mx * scale;
-    if (__any(mt > m + 8.0f)) {
-      const float mnew = fmaxf(m, mt);
+    // Reference max, kept in the scaled log2 domain: m is the row max of the
+    // first tile (key 0 is visible to every row) and is raised only when a
+    // later tile's p = 2^(s*scale - m) would exceed 2^20.  Each lane's p sum
+    // bounds its p values, so no per-tile max is taken on the common path;
+    // p up to 2^20 is exact to bf16 rounding and O, l cannot overflow.  An
+    // overflowed or non-finite sum also takes the rescale branch, which
+    // recomputes P against the new max.
+    auto row_max = [&]() {
+      float mx = s0[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+      mx = wave_max_xor(mx, 32);
+      return mx * scale;
+    };
+    if (t == 0) m = row_max();
+    float psum = 0.f;
+    bf16x8 pb[2];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale, -m));
+      psum += p0;
+      pb[r >> 3][r & 7] = f2bf(p0);
+    }
+    if (__any(!(psum <= 1048576.0f))) {
+      const float mnew = fmaxf(m, row_max());
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       l *= alpha;
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] *= alpha;
       m = mnew;
-    }
-    const float mnew = m;
-    float psum = 0.f;
-    bf16x8 pb[2];
+      psum = 0.f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale, -mnew));
-      psum += p0;
-      pb[r >> 3][r & 7] = f2bf(p0);
+      for (int r = 0; r < 16; ++r) {
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[r], scale, -m));
+        psum += p0;
+        pb[r >> 3][r & 7] = f2bf(p0);
+      }
     }
     l += psum;
 

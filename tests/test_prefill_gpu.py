@@ -95,3 +95,36 @@ def test_provider_mirror_and_errors(gpu):
     ref = O.prefill_attention(q, k, v, 0, out_dtype=torch.float32)
     assert (out.cpu() - ref).abs().max().item() <= TOL_TIGHT
     prov.release()
+
+
+@pytest.mark.parametrize("t,s", [(256, 256), (300, 1500)])
+def test_prefill_rising_scores_rescale(gpu, t, s):
+    """Key norms grow along the sequence, so every row's running max keeps
+    rising tile after tile and the kernel's rescale branch (O and l moved to
+    a new reference max) runs repeatedly."""
+    from qwen36_attn.full_attention import fmha_prefill
+    q, k, v = _inputs(t, s, seed=11 + t)
+    growth = torch.linspace(0.05, 6.0, s).view(s, 1, 1)
+    k = (k.float() * growth).to(torch.bfloat16)
+    print(f"prefill rising T={t} S={s}", flush=True)
+    got = fmha_prefill(q.to(gpu), k.to(gpu), v.to(gpu)).cpu()
+    ref = O.prefill_attention(q, k, v, position_start=s - t, out_dtype=torch.float32)
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max().item() <= TOL
+
+
+def test_prefill_overflowing_jump_rescale(gpu):
+    """Tiny keys in the first tile, then keys ~10^4 times larger: the first
+    probabilities computed against the first tile's max overflow to inf, and
+    the rescale branch must recompute them against the new max."""
+    from qwen36_attn.full_attention import fmha_prefill
+    t = s = 200
+    q, k, v = _inputs(t, s, seed=5)
+    scale = torch.full((s, 1, 1), 60.0)
+    scale[:32] = 0.005
+    k = (k.float() * scale).to(torch.bfloat16)
+    print("prefill overflow jump", flush=True)
+    got = fmha_prefill(q.to(gpu), k.to(gpu), v.to(gpu)).cpu()
+    ref = O.prefill_attention(q, k, v, position_start=0, out_dtype=torch.float32)
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max().item() <= TOL
