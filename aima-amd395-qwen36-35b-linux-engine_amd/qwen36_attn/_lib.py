@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
                                         _vp, _vp, _vp, _u32, _vp, _sz, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
+    "qwen36_gdn_decode_step": (_i32, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _vp,
+                                      _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
 }
 
 _LIB = None

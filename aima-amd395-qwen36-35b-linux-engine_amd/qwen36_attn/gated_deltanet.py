@@ -158,6 +158,54 @@ def gated_rmsnorm(core: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> 
     return out
 
 
+def gdn_decode_step(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
+                    new_conv_state: torch.Tensor, conv_weight: torch.Tensor,
+                    a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
+                    dt_bias: torch.Tensor, z: torch.Tensor, norm_weight: torch.Tensor,
+                    ssm_state: torch.Tensor, final_state: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """One fused launch for the decode part of ``linear_attention`` between
+    the input projections and out_proj (fle:6378-6544, mode "decode"): conv
+    + SiLU, gating, l2norm, recurrent delta rule and gated RMSNorm for the
+    T rows of ``mixed_qkv``.  ``new_conv_state`` receives the conv state and
+    must be a different buffer from ``conv_state``; ``final_state`` (default:
+    ``ssm_state`` itself) receives the fp32 recurrent state.  Returns the
+    gated output [T, 4096] bf16."""
+    t = mixed_qkv.shape[0]
+    require(mixed_qkv, "mixed_qkv", torch.bfloat16, contiguous=False)
+    if mixed_qkv.shape[1] != CONV_DIM or mixed_qkv.stride(1) != 1:
+        raise ValueError("mixed_qkv must be [T, 8192] with unit inner stride")
+    require(conv_state, "conv_state", torch.bfloat16, shape=(CONV_DIM, 3))
+    require(new_conv_state, "new_conv_state", torch.bfloat16, shape=(CONV_DIM, 3))
+    if new_conv_state.data_ptr() == conv_state.data_ptr():
+        raise ValueError("new_conv_state must not alias conv_state (double-buffer it)")
+    require(conv_weight, "conv_weight", torch.bfloat16, shape=(CONV_DIM, 4))
+    for name, x in (("a", a), ("b", b)):
+        require(x, name, torch.bfloat16, contiguous=False)
+        if x.shape != (t, HV) or x.stride(1) != 1:
+            raise ValueError(f"{name} must be [T, 32]")
+    if a.stride(0) != b.stride(0):
+        raise ValueError("a and b must share a row stride")
+    require(z, "z", torch.bfloat16, contiguous=False)
+    if z.shape != (t, VALUE_DIM) or z.stride(1) != 1:
+        raise ValueError("z must be [T, 4096] with unit inner stride")
+    require(norm_weight, "norm_weight", torch.bfloat16, shape=(DV,))
+    ssm = ssm_state.reshape(HV, DK, DV)
+    require(ssm, "ssm_state", torch.float32)
+    if final_state is None:
+        final_state = ssm
+    require(final_state.reshape(HV, DK, DV), "final_state", torch.float32)
+    a_log = a_log.float().contiguous()
+    dt_bias = dt_bias.float().contiguous()
+    if out is None:
+        out = torch.empty(t, VALUE_DIM, dtype=torch.bfloat16, device=mixed_qkv.device)
+    _lib.call("qwen36_gdn_decode_step", ptr(mixed_qkv), mixed_qkv.stride(0), ptr(conv_weight),
+              ptr(conv_state), ptr(new_conv_state), ptr(a), ptr(b), a.stride(0), ptr(a_log),
+              ptr(dt_bias), ptr(z), z.stride(0), ptr(norm_weight), ptr(ssm), ptr(final_state),
+              ptr(out), t, stream_handle(out.device))
+    return out
+
+
 class LinearAttentionLayer:
     """One Gated-DeltaNet layer with its carried conv and recurrent states,
     mirroring ``linear_attention(inp, layer_index, weights)``
@@ -171,13 +219,24 @@ class LinearAttentionLayer:
         self.w = weights
         self.conv_state = torch.zeros(CONV_DIM, 3, dtype=torch.bfloat16, device=device)
         self.ssm_state = torch.zeros(HV, DK, DV, dtype=torch.float32, device=device)
+        self.conv_spare = None   # second conv-state buffer for the fused decode step
 
-    def forward(self, inp: torch.Tensor, mode: str) -> torch.Tensor:
+    def forward(self, inp: torch.Tensor, mode: str, fused: bool = True) -> torch.Tensor:
+        """``mode == "decode"`` runs the fused one-launch step
+        (``gdn_decode_step``) unless ``fused`` is False, which runs the same
+        step as four launches (conv, gating, recurrent, gated norm)."""
         w = self.w
         mixed = inp @ w["in_proj_qkv"].t()
         z = inp @ w["in_proj_z"].t()
         b = inp @ w["in_proj_b"].t()
         a = inp @ w["in_proj_a"].t()
+        if mode == "decode" and fused:
+            if self.conv_spare is None:
+                self.conv_spare = torch.empty_like(self.conv_state)
+            gated = gdn_decode_step(mixed, self.conv_state, self.conv_spare, w["conv1d"], a, b,
+                                    w["A_log"], w["dt_bias"], z, w["norm"], self.ssm_state)
+            self.conv_state, self.conv_spare = self.conv_spare, self.conv_state
+            return gated @ w["out_proj"].t()
         conv_out, _ = causal_conv1d(mixed, self.conv_state, w["conv1d"], new_state=self.conv_state)
         t = conv_out.shape[0]
         q = conv_out[:, :KEY_DIM].view(t, HK, DK)

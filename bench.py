@@ -219,6 +219,52 @@ def bench_gdn_recurrent(torch, dev, layers, iters, warmup, use_graph, seed=2):
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_gdn_decode_step(torch, dev, layers, iters, warmup, use_graph, fused=True, seed=4):
+    """Everything between a GDN layer's input projections and out_proj for
+    one decode token (conv, gating, l2norm, recurrent delta rule, gated
+    RMSNorm), through 30 layers with their own states: one fused launch per
+    layer (``fused``) or the four-launch sequence conv / gating / recurrent /
+    gated norm."""
+    from qwen36_attn import gated_deltanet as G
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(seed)
+    L = []
+    for _ in range(layers):
+        L.append(dict(
+            mixed=syn.randn((1, 8192), g).to(dev), conv_w=syn.randn((8192, 4), g, 0.5).to(dev),
+            conv_a=syn.randn((8192, 3), g).to(dev), conv_b=syn.randn((8192, 3), g).to(dev),
+            a=syn.randn((1, 32), g).to(dev), b=syn.randn((1, 32), g).to(dev),
+            a_log=torch.log(torch.rand(32, generator=g) * 16 + 1e-4).float().to(dev),
+            dt_bias=torch.randn(32, generator=g).float().to(dev), z=syn.randn((1, 4096), g).to(dev),
+            norm=syn.randn((128,), g, 0.5).to(dev),
+            ssm=(torch.randn(32, 128, 128, generator=g) * 0.2).to(dev),
+            out=torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)))
+
+    def step():
+        for d in L:
+            if fused:
+                G.gdn_decode_step(d["mixed"], d["conv_a"], d["conv_b"], d["conv_w"], d["a"], d["b"],
+                                  d["a_log"], d["dt_bias"], d["z"], d["norm"], d["ssm"],
+                                  out=d["out"])
+            else:
+                conv_out, _ = G.causal_conv1d(d["mixed"], d["conv_a"], d["conv_w"],
+                                              new_state=d["conv_b"])
+                q = conv_out[:, :2048].view(1, 16, 128)
+                k = conv_out[:, 2048:4096].view(1, 16, 128)
+                v = conv_out[:, 4096:].view(1, 32, 128)
+                gg, beta = G.gating(d["a"], d["b"], d["a_log"], d["dt_bias"])
+                core, _ = G.recurrent_gated_delta_rule(q, k, v, gg, beta, d["ssm"],
+                                                       final_state=d["ssm"])
+                d["out"] = G.gated_rmsnorm(core, d["z"], d["norm"])
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    nbytes = GDN_STATE_BYTES * layers
+    return {"layers": layers, "launches_per_layer": 1 if fused else 4, "us_per_token": us,
+            "hbm_gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_gdn_prefill(torch, dev, t, iters, warmup, seed=3):
     """Config 4: chunked delta-rule prefill of T tokens from zero state."""
     from qwen36_attn import gated_deltanet as G
@@ -274,6 +320,7 @@ def run_only(torch, fa, dev, args):
              bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup)]
     elif args.only == "gdn":
         r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
+             bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
     else:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev)
@@ -311,6 +358,9 @@ def main():
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
+        "gdn_decode_step_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5, use_graph),
+        "gdn_decode_unfused_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5,
+                                                             use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
     }
     extra["attention_us_per_token_128k"] = (head["us_per_token"]

@@ -145,6 +145,28 @@ int qwen36_gdn_gated_norm(const void* core, const void* z,
                           unsigned z_row_stride, const void* weight, void* out,
                           unsigned tokens, void* stream);
 
+/* qwen36_gdn_decode_step: one launch for everything between the GDN input
+ *   projections and out_proj -- conv1d + SiLU, gating, l2norm, the recurrent
+ *   delta rule and the gated RMSNorm -- for `tokens` consecutive tokens.
+ *   Replaces the reference decode's launch sequence for the linear layer
+ *   (native_linear_layer.hip.cpp:84-157: fused input-projection/conv,
+ *   fused_sigmoid_gating_delta_rule_update, gated norm; torch form
+ *   four_layer_mini_engine.py:6378-6544 with mode == "decode").
+ *   mixed_qkv [T, >=8192 stride] bf16 (before the conv), conv_weight
+ *   [8192,4], conv_state_in -> conv_state_out [8192,3] bf16 (must not
+ *   overlap: double-buffer them), a, b [T, >=32 stride] bf16, A_log, dt_bias
+ *   [32] fp32, z [T, >=4096 stride] bf16, norm_weight [128] bf16,
+ *   state_in -> state_out [32,128,128] fp32 (may alias), out [T,4096] bf16.
+ *   Same error convention as the other entry points. */
+int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
+                           const void* conv_weight, const void* conv_state_in,
+                           void* conv_state_out, const void* a, const void* b,
+                           unsigned ab_row_stride, const void* a_log,
+                           const void* dt_bias, const void* z,
+                           unsigned z_row_stride, const void* norm_weight,
+                           const void* state_in, void* state_out, void* out,
+                           unsigned tokens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,6 +76,20 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qwen36_rotary_table(None, None, 1, 0, None) == 1
     assert L.qwen36_gdn_gated_norm(1, 1, 100, 1, 1, 1, None) == 1
     assert L.qwen36_gdn_gating(1, 1, 8, 1, 1, 1, 1, 1, None) == 1
+    # fused GDN decode step: aliased / overlapping conv state, bad strides, T = 0
+    good = dict(x=16, xs=8192, w=32, ci=4096, co=1 << 20, a=48, b=64, abs_=32, al=80, dt=96,
+                z=128, zs=4096, nw=160, si=256, so=256, out=512)
+    def step(**kw):
+        v = dict(good, **kw)
+        return L.qwen36_gdn_decode_step(v["x"], v["xs"], v["w"], v["ci"], v["co"], v["a"], v["b"],
+                                        v["abs_"], v["al"], v["dt"], v["z"], v["zs"], v["nw"],
+                                        v["si"], v["so"], v["out"], v.get("t", 1), None)
+    assert step(co=4096) == 1                 # conv_state_out == conv_state_in
+    assert step(co=4096 + 2 * 8192 * 3 - 2) == 1   # overlapping conv buffers
+    assert step(xs=100) == 1
+    assert step(zs=100) == 1
+    assert step(abs_=8) == 1
+    assert step(t=0) == 1
 
 
 def test_fixtures_match_oracle():
