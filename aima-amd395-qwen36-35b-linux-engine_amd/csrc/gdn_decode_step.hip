@@ -29,8 +29,12 @@
 namespace q36 {
 namespace {
 
-constexpr int kDsThreads = 512;
-constexpr int kDsRowsPerThread = 8;     // 16 row groups x 8 rows = 128
+#ifndef DS_THREADS
+#define DS_THREADS 512   // 1024 measured 14% slower (more waves, same per-CU bytes)
+#endif
+constexpr int kDsThreads = DS_THREADS;
+constexpr int kDsWaves = kDsThreads / 64;
+constexpr int kDsRowsPerThread = kGdnDk / (kDsThreads / 32);   // row groups of 32 threads
 
 __device__ __forceinline__ float ds_mul(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float ds_add(float a, float b) { return __fadd_rn(a, b); }
@@ -46,7 +50,7 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
     bf16* __restrict__ out, unsigned tokens) {
   __shared__ float ych[2][3 * kGdnDk];              // [parity][q | k | v] conv outputs
   __shared__ float gb[2][2];                        // [parity][g, beta]
-  __shared__ f32x4 red[2][8][2][32];                // [parity][wave][kv | sq][col quad]
+  __shared__ f32x4 red[2][kDsWaves][2][32];         // [parity][wave][kv | sq][col quad]
   const int h = blockIdx.x;
   const int kh = h >> 1;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -139,7 +143,7 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
     __syncthreads();
     f32x4 kv_raw = red[par][0][0][cq], sq_raw = red[par][0][1][cq];
 #pragma unroll
-    for (int wv = 1; wv < 8; ++wv) {
+    for (int wv = 1; wv < kDsWaves; ++wv) {
       kv_raw += red[par][wv][0][cq];
       sq_raw += red[par][wv][1][cq];
     }
