@@ -19,6 +19,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <math.h>
 
 namespace q36 {
 
@@ -87,6 +88,68 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+
+// ---- head RMSNorm + partial RoPE (shared by the prefill pointwise kernel
+// and the fused decode step, so both round identically) -------------------
+// RoPE inverse frequencies 1 / 1e7^(2i/64), i < 32, each correctly rounded
+// to fp32 (computed on the host in double; each translation unit keeps its
+// own __constant__ copy).
+inline void rope_inv_freq_host(float* h) {
+  for (int i = 0; i < kRotaryPairs; ++i)
+    h[i] = (float)(1.0 / pow(1.0e7, (2.0 * i) / (double)kRotary));
+}
+
+// RoPE cos/sin for one position as one wave needs them: lane p < 32 computes
+// pair p (fp32 angle = pos * inv_freq[p], cosf/sinf), and lane l < 16 then
+// gathers pairs (4l + e) mod 32, e < 4 -- the pairs of its dims 4l..4l+3.
+__device__ __forceinline__ void rope_cos_sin_wave(unsigned pos, const float* inv_freq,
+                                                  float (&c)[4], float (&s)[4]) {
+  const int lane = threadIdx.x & 63;
+  const float angle = __fmul_rn((float)pos, inv_freq[lane & (kRotaryPairs - 1)]);
+  const float cv = cosf(angle), sv = sinf(angle);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    c[e] = __shfl(cv, (4 * lane + e) & (kRotaryPairs - 1), 64);
+    s[e] = __shfl(sv, (4 * lane + e) & (kRotaryPairs - 1), 64);
+  }
+}
+
+// One 256-wide head held by one wave, lane l holding dims 4l..4l+3: RMSNorm
+// with the (w + 1) weight (fp32, every product and sum rounded separately,
+// eps 1e-6, correctly rounded rsqrt), rounded to bf16, then rotate-half RoPE
+// on dims [0, 64) with the cos/sin of rope_cos_sin_wave (lanes 0-7 pair with
+// lanes 8-15).
+// Returns the fp32 values before the final bf16 rounding.
+// (four_layer_mini_engine.py:5151-5162; native_pointwise.hip.cpp:242-337.)
+__device__ __forceinline__ void head_norm_rope_wave(const float (&x)[4],
+                                                    const bf16* __restrict__ w,
+                                                    const float (&cs)[4],
+                                                    const float (&sn)[4],
+                                                    float (&y)[4]) {
+  const int lane = threadIdx.x & 63;
+  float sq[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) sq[e] = __fmul_rn(x[e], x[e]);
+  float sum = __fadd_rn(__fadd_rn(sq[0], sq[1]), __fadd_rn(sq[2], sq[3]));
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, o, 64));
+  const float var = __fmul_rn(sum, 1.0f / 256.0f);
+  const float inv = (float)(1.0 / sqrt((double)__fadd_rn(var, 1e-6f)));
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float wp1 = __fadd_rn(bf2f(w[4 * lane + e]), 1.0f);
+    y[e] = bf2f(f2bf(__fmul_rn(__fmul_rn(x[e], inv), wp1)));
+  }
+  float mate[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) mate[e] = __shfl_xor(y[e], 8, 64);
+  if (lane < 16) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      y[e] = lane < 8 ? __fsub_rn(__fmul_rn(y[e], cs[e]), __fmul_rn(mate[e], sn[e]))
+                      : __fadd_rn(__fmul_rn(y[e], cs[e]), __fmul_rn(mate[e], sn[e]));
+  }
 }
 
 }  // namespace q36

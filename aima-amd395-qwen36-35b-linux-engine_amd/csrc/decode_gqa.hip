@@ -45,6 +45,21 @@ constexpr unsigned kMaxSplits = 256;
 // -- and 64..192; one workgroup holding both KV heads was no faster.)
 constexpr unsigned kTargetSplits = 128;
 
+// RoPE inverse frequencies for the fused decode step (this translation
+// unit's copy; see rope_inv_freq_host).
+__constant__ float c_dec_inv_freq[kRotaryPairs];
+
+// Raw inputs of the fused decode step (qwen36_decode_step): the q-projection
+// row [16 heads x (256 query | 256 gate)], the raw k and v rows [2 x 256]
+// and the head-norm weights.  Unused (null) for qwen36_decode_gqa.
+struct FuseArgs {
+  const bf16* q_gate;
+  const bf16* k_raw;
+  const bf16* v_raw;
+  const bf16* q_w;
+  const bf16* k_w;
+};
+
 // Workspace carve-up (fp32).
 struct DecodeWs {
   float* o;            // [2][nsplit][8][256] split partials (unnormalised)
@@ -62,11 +77,12 @@ __device__ __forceinline__ void store_partial(float* o, float* ml,
   }
 }
 
+template <bool kFuse>
 __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     const bf16* __restrict__ q, bf16* __restrict__ k_cache,
     bf16* __restrict__ v_cache, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
-    unsigned split_tokens, unsigned nsplit, DecodeWs ws) {
+    unsigned split_tokens, unsigned nsplit, DecodeWs ws, FuseArgs fz) {
   __shared__ __attribute__((aligned(16))) char lds[kDecLds];
   const int kvh = blockIdx.y;
   const unsigned split = blockIdx.x;
@@ -84,7 +100,54 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // The workgroup that owns the new row's block writes it to the cache (this
   // KV head's half) and reads K/V for that token from k_new/v_new directly,
   // so no other workgroup depends on the write.
-  const bool has_new = k_new != nullptr && (position / kDecBlock) % nsplit == split;
+  const bool owner = (position / kDecBlock) % nsplit == split;
+  const bool has_new = !kFuse && k_new != nullptr && owner;
+  // Fused step: the owner writes the new row -- K after head norm and RoPE,
+  // V raw -- and is its only reader, so it then streams that row from the
+  // cache like every other.  If the row lies in one of the first blocks
+  // (round < 4: short caches) the write completes before any load is issued;
+  // otherwise it overlaps the first loads and the workgroup barrier after Q
+  // staging orders it before the row's block is read.
+  // Raw inputs of the fused step are requested before the first K/V block so
+  // that their (short) round trip does not queue behind it.
+  float xq[2][4], xk[4];
+  bf16x4 vrow;
+  if constexpr (kFuse) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const bf16x4 r = *reinterpret_cast<const bf16x4*>(
+          fz.q_gate + (size_t)(kvh * kGroup + 2 * wave + u) * 2 * kD + 4 * lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xq[u][e] = bf2f(r[e]);
+    }
+    if (owner && wave == 0) {
+      const bf16x4 r = *reinterpret_cast<const bf16x4*>(fz.k_raw + kvh * kD + 4 * lane);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xk[e] = bf2f(r[e]);
+    }
+    if (owner && wave == 1) vrow = *reinterpret_cast<const bf16x4*>(fz.v_raw + kvh * kD + 4 * lane);
+  }
+  auto write_new_row = [&]() {
+    const size_t o = ((size_t)position * kHkv + kvh) * kD;
+    if (wave == 0) {
+      float y[4];
+      float cs[4], sn[4];
+      rope_cos_sin_wave(position, c_dec_inv_freq, cs, sn);
+      head_norm_rope_wave(xk, fz.k_w, cs, sn, y);
+      bf16x4 yb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) yb[e] = f2bf(y[e]);
+      *reinterpret_cast<bf16x4*>(k_cache + o + 4 * lane) = yb;
+    } else if (wave == 1) {
+      *reinterpret_cast<bf16x4*>(v_cache + o + 4 * lane) = vrow;
+    }
+  };
+  const bool early_row = kFuse && owner && (position / kDecBlock) / nsplit < (unsigned)kDecWaves;
+  if (early_row) {
+    write_new_row();
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
   if (has_new && wave == 0) {
     const size_t o = ((size_t)position * kHkv + kvh) * kD;
     if (lane < 32) {
@@ -159,7 +222,28 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // dims s*32 + 8*lg .. +8, so one K load instruction reads 16 rows x 64
   // contiguous bytes.
   char* qs = lds + kVLds;
-  {
+  if constexpr (kFuse) {
+    if (owner && !early_row) write_new_row();
+    // Head norm + RoPE of this group's 8 query heads (wave w: heads 2w,
+    // 2w+1) straight into the Q^T operand rows; rows 8..15 are zero padding.
+    float cs[4], sn[4];
+    rope_cos_sin_wave(position, c_dec_inv_freq, cs, sn);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int hh = 2 * wave + u;
+      float y[4];
+      head_norm_rope_wave(xq[u], fz.q_w, cs, sn, y);
+      bf16x4 yb;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) yb[e] = f2bf(y[e]);
+      *reinterpret_cast<bf16x4*>(qs + hh * kQPitch + 8 * lane) = yb;
+    }
+    {
+      const int r = kGroup + (threadIdx.x >> 5), c = threadIdx.x & 31;
+      *reinterpret_cast<uint4*>(qs + r * kQPitch + c * 16) = uint4{0u, 0u, 0u, 0u};
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the new row's stores complete before the barrier
+  } else {
     const int r = threadIdx.x >> 4, c = threadIdx.x & 15;   // 16 rows x 16 chunks
     uint4 a = uint4{0u, 0u, 0u, 0u}, b = uint4{0u, 0u, 0u, 0u};
     if (r < kGroup) {
@@ -379,6 +463,47 @@ Q36_EXPORT size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
   return workspace_bytes((cache_end + per - 1) / per);
 }
 
+static int launch_decode(bool fuse, const void* q, const void* k_new,
+                         const void* v_new, const FuseArgs& fz, void* k_cache,
+                         void* v_cache, unsigned position, unsigned cache_end,
+                         unsigned capacity, const void* gate,
+                         unsigned gate_head_stride, void* out, void* workspace,
+                         size_t workspace_bytes_given, unsigned split_tokens,
+                         void* stream) {
+  const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
+  const unsigned nsplit = (cache_end + per - 1) / per;
+  if (nsplit > kMaxSplits) return Q36_EINVAL;
+  if (workspace_bytes_given < workspace_bytes(nsplit)) return Q36_EINVAL;
+  DecodeWs ws;
+  ws.o = static_cast<float*>(workspace);
+  ws.ml = ws.o + (size_t)nsplit * kHkv * kGroup * kD;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto kernel = fuse ? decode_gqa_split_kernel<true> : decode_gqa_split_kernel<false>;
+  hipLaunchKernelGGL(kernel, dim3(nsplit, kHkv), dim3(256), 0, st,
+                     static_cast<const bf16*>(q), static_cast<bf16*>(k_cache),
+                     static_cast<bf16*>(v_cache), static_cast<const bf16*>(k_new),
+                     static_cast<const bf16*>(v_new), position, cache_end, per,
+                     nsplit, ws, fz);
+  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / kCombineDims), dim3(256),
+                     0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
+                     gate_head_stride, static_cast<bf16*>(out));
+  return static_cast<int>(hipGetLastError());
+}
+
+static bool g_dec_freq_ready[64] = {};
+
+static int ensure_dec_inv_freq() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return Q36_EINVAL;
+  if (g_dec_freq_ready[dev]) return Q36_OK;
+  float h[kRotaryPairs];
+  rope_inv_freq_host(h);
+  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(c_dec_inv_freq), h, sizeof(h));
+  if (e != hipSuccess) return (int)e;
+  g_dec_freq_ready[dev] = true;
+  return Q36_OK;
+}
+
 Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
                                  const void* v_new, void* k_cache,
                                  void* v_cache, unsigned position,
@@ -394,22 +519,40 @@ Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
       (k_new != nullptr && position >= cache_end) ||
       (split_tokens % (kDecWaves * kDecBlock)) != 0)
     return Q36_EINVAL;
-  const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
-  const unsigned nsplit = (cache_end + per - 1) / per;
-  if (nsplit > kMaxSplits) return Q36_EINVAL;
-  if (workspace_bytes_given < workspace_bytes(nsplit)) return Q36_EINVAL;
-  DecodeWs ws;
-  ws.o = static_cast<float*>(workspace);
-  ws.ml = ws.o + (size_t)nsplit * kHkv * kGroup * kD;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(decode_gqa_split_kernel, dim3(nsplit, kHkv), dim3(256), 0,
-                     st, static_cast<const bf16*>(q),
-                     static_cast<bf16*>(k_cache), static_cast<bf16*>(v_cache),
-                     static_cast<const bf16*>(k_new),
-                     static_cast<const bf16*>(v_new), position, cache_end, per,
-                     nsplit, ws);
-  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / kCombineDims), dim3(256),
-                     0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
-                     gate_head_stride, static_cast<bf16*>(out));
-  return static_cast<int>(hipGetLastError());
+  return launch_decode(false, q, k_new, v_new, FuseArgs{}, k_cache, v_cache, position,
+                       cache_end, capacity, gate, gate_head_stride, out, workspace,
+                       workspace_bytes_given, split_tokens, stream);
+}
+
+Q36_EXPORT int qwen36_decode_step(const void* q_gate, const void* k_raw,
+                                  const void* v_raw, const void* q_norm_weight,
+                                  const void* k_norm_weight, void* k_cache,
+                                  void* v_cache, unsigned position,
+                                  unsigned cache_end, unsigned capacity,
+                                  void* out, void* workspace,
+                                  size_t workspace_bytes_given,
+                                  unsigned split_tokens, void* stream) {
+  if (q_gate == nullptr || k_raw == nullptr || v_raw == nullptr ||
+      q_norm_weight == nullptr || k_norm_weight == nullptr || k_cache == nullptr ||
+      v_cache == nullptr || out == nullptr || workspace == nullptr || cache_end == 0 ||
+      cache_end > capacity || capacity > kMaxTokens || position >= cache_end ||
+      (split_tokens % (kDecWaves * kDecBlock)) != 0 ||
+      (reinterpret_cast<uintptr_t>(q_gate) % 8) != 0 ||
+      (reinterpret_cast<uintptr_t>(k_raw) % 8) != 0 ||
+      (reinterpret_cast<uintptr_t>(v_raw) % 8) != 0 ||
+      (reinterpret_cast<uintptr_t>(k_cache) % 8) != 0 ||
+      (reinterpret_cast<uintptr_t>(v_cache) % 8) != 0)
+    return Q36_EINVAL;
+  const int st = ensure_dec_inv_freq();
+  if (st != Q36_OK) return st;
+  FuseArgs fz;
+  fz.q_gate = static_cast<const bf16*>(q_gate);
+  fz.k_raw = static_cast<const bf16*>(k_raw);
+  fz.v_raw = static_cast<const bf16*>(v_raw);
+  fz.q_w = static_cast<const bf16*>(q_norm_weight);
+  fz.k_w = static_cast<const bf16*>(k_norm_weight);
+  // The gate is the second half of each head's 512-wide q-projection slice.
+  return launch_decode(true, nullptr, nullptr, nullptr, fz, k_cache, v_cache, position,
+                       cache_end, capacity, static_cast<const bf16*>(q_gate) + kD, 2 * kD,
+                       out, workspace, workspace_bytes_given, split_tokens, stream);
 }

@@ -23,13 +23,6 @@ namespace {
 __constant__ float c_inv_freq[kRotaryPairs];
 
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-__device__ __forceinline__ float sub_rn(float a, float b) { return __fsub_rn(a, b); }
-
-// Correctly rounded fp32 reciprocal square root via fp64.
-__device__ __forceinline__ float rsqrt_rn(float x) {
-  return (float)(1.0 / sqrt((double)x));
-}
 
 __global__ void rotary_table_kernel(float* __restrict__ cosv,
                                     float* __restrict__ sinv, unsigned tokens,
@@ -60,39 +53,12 @@ __global__ __launch_bounds__(64) void head_norm_rope_kernel(
                          : k_raw + (size_t)t * k_row_stride + head * kD;
   const bf16* w = is_q ? q_weight : k_weight;
 
-  float x[4], sq[4];
+  float x[4], y[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    x[e] = bf2f(src[4 * lane + e]);
-    sq[e] = mul_rn(x[e], x[e]);
-  }
-  float sum = add_rn(add_rn(sq[0], sq[1]), add_rn(sq[2], sq[3]));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) sum = add_rn(sum, __shfl_xor(sum, o, 64));
-  const float var = mul_rn(sum, 1.0f / 256.0f);
-  const float inv = rsqrt_rn(add_rn(var, 1e-6f));
-
-  float y[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float wp1 = add_rn(bf2f(w[4 * lane + e]), 1.0f);
-    y[e] = bf2f(f2bf(mul_rn(mul_rn(x[e], inv), wp1)));
-  }
-  // RoPE on dims [0, 64): lane < 8 pairs with lane + 8.
-  float mate[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) mate[e] = __shfl_xor(y[e], 8, 64);
-  if (lane < 16) {
-    const float pos = (float)(position_start + t);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int pair = (4 * lane + e) & (kRotaryPairs - 1);
-      const float angle = mul_rn(pos, c_inv_freq[pair]);
-      const float c = cosf(angle), s = sinf(angle);
-      y[e] = lane < 8 ? sub_rn(mul_rn(y[e], c), mul_rn(mate[e], s))
-                      : add_rn(mul_rn(y[e], c), mul_rn(mate[e], s));
-    }
-  }
+  for (int e = 0; e < 4; ++e) x[e] = bf2f(src[4 * lane + e]);
+  float cs[4], sn[4];
+  rope_cos_sin_wave(position_start + t, c_inv_freq, cs, sn);
+  head_norm_rope_wave(x, w, cs, sn, y);
   const size_t pos = position_start + t;
   bf16* dst = is_q ? q_out + ((size_t)t * kHq + head) * kD
                    : k_cache + (pos * kHkv + head) * kD;
@@ -130,8 +96,7 @@ int ensure_inv_freq() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return Q36_EINVAL;
   if (g_freq_ready[dev]) return Q36_OK;
   float h[kRotaryPairs];
-  for (int i = 0; i < kRotaryPairs; ++i)
-    h[i] = (float)(1.0 / pow(1.0e7, (2.0 * i) / (double)kRotary));
+  rope_inv_freq_host(h);
   const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(c_inv_freq), h, sizeof(h));
   if (e != hipSuccess) return (int)e;
   g_freq_ready[dev] = true;

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_decode_gqa_workspace_bytes": (_sz, [_u32, _u32]),
     "qwen36_decode_gqa": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                  _vp, _u32, _vp, _vp, _sz, _u32, _vp]),
+    "qwen36_decode_step": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                  _vp, _vp, _sz, _u32, _vp]),
     # pointwise (full attention)
     "qwen36_rotary_table": (_i32, [_vp, _vp, _u32, _u32, _vp]),
     "qwen36_head_norm_rope": (_i32, [_vp, _u32, _vp, _u32, _vp, _u32, _vp, _vp,

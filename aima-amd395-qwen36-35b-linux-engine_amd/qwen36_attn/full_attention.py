@@ -64,7 +64,12 @@ def decode_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         require(gate, "gate", torch.bfloat16, contiguous=False)
         if gate.numel() != Q_DIM or gate.stride(-1) != 1:
             raise ValueError("gate must hold 4096 values with unit inner stride")
-        gate_stride = HEAD_DIM
+        if gate.dim() == 2 and gate.shape == (HQ, HEAD_DIM):
+            gate_stride = gate.stride(0)      # e.g. the gate half of [16, 512] q rows
+        elif gate.is_contiguous():
+            gate_stride = HEAD_DIM
+        else:
+            raise ValueError("gate must be contiguous [4096] or a [16, 256] view with unit inner stride")
     if out is None:
         out = torch.empty(1, Q_DIM, dtype=torch.bfloat16, device=dev)
     require(out, "out", torch.bfloat16)
@@ -74,6 +79,46 @@ def decode_gqa(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     _lib.call("qwen36_decode_gqa", ptr(q), ptr(k_new), ptr(v_new), ptr(k_cache),
               ptr(v_cache), position, cache_end, capacity, ptr(gate), gate_stride,
               ptr(out), ptr(ws), ws.numel(), split_tokens, stream_handle(dev))
+    return out
+
+
+def decode_step(q_gate: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                q_norm: torch.Tensor, k_norm: torch.Tensor, k_cache: torch.Tensor,
+                v_cache: torch.Tensor, position: int, cache_end: int | None = None,
+                out: torch.Tensor | None = None, split_tokens: int = 0) -> torch.Tensor:
+    """The whole one-token decode of the gated full-attention layer between
+    its projections and o_proj (four_layer_mini_engine.py:6546-6653, mode
+    "decode") in one fused split launch plus the combine: head norm + RoPE
+    of q and the new k, the cache-row write at ``position`` (K normalised, V
+    raw), split-K attention over rows [0, cache_end) and the sigmoid output
+    gate.  q_gate [1, 8192] (or [8192]) is the fused q projection row; k, v
+    [1, 512] raw; returns [1, 4096] bf16.  Same rounding as
+    ``head_norm_rope_kv_write`` followed by ``decode_gqa``."""
+    dev = q_gate.device
+    if cache_end is None:
+        cache_end = position + 1
+    for name, x, n in (("q_gate", q_gate, 2 * Q_DIM), ("k", k, KV_DIM), ("v", v, KV_DIM)):
+        require(x, name, torch.bfloat16)
+        if x.numel() != n:
+            raise ValueError(f"{name} must hold {n} values")
+    require(q_norm, "q_norm", torch.bfloat16, shape=(HEAD_DIM,))
+    require(k_norm, "k_norm", torch.bfloat16, shape=(HEAD_DIM,))
+    require(k_cache, "k_cache", torch.bfloat16)
+    require(v_cache, "v_cache", torch.bfloat16)
+    if k_cache.dim() != 3 or tuple(k_cache.shape[1:]) != (HKV, HEAD_DIM) or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache/v_cache must be [capacity, 2, 256]")
+    capacity = k_cache.shape[0]
+    if not (0 <= position < cache_end <= capacity):
+        raise ValueError("native grouped attention geometry is invalid")
+    if out is None:
+        out = torch.empty(1, Q_DIM, dtype=torch.bfloat16, device=dev)
+    require(out, "out", torch.bfloat16)
+    lib = _lib.load(("qwen36_decode_step",))
+    ws_bytes = lib.qwen36_decode_gqa_workspace_bytes(cache_end, split_tokens)
+    ws = scratch("decode_gqa", ws_bytes, dev)
+    _lib.call("qwen36_decode_step", ptr(q_gate), ptr(k), ptr(v), ptr(q_norm), ptr(k_norm),
+              ptr(k_cache), ptr(v_cache), position, cache_end, capacity, ptr(out), ptr(ws),
+              ws.numel(), split_tokens, stream_handle(dev))
     return out
 
 
@@ -216,7 +261,11 @@ class FullAttentionLayer:
         self.k_cache = torch.zeros(capacity, HKV, HEAD_DIM, dtype=torch.bfloat16, device=device)
         self.v_cache = torch.zeros_like(self.k_cache)
 
-    def forward(self, inp: torch.Tensor, position_start: int, mode: str) -> torch.Tensor:
+    def forward(self, inp: torch.Tensor, position_start: int, mode: str,
+                fused: bool = True) -> torch.Tensor:
+        """``mode == "decode"`` runs the fused step (``decode_step``: norm,
+        RoPE, KV write, attention and gate in the split + combine launches)
+        unless ``fused`` is False (separate head-norm/RoPE launch)."""
         t = inp.shape[0]
         if position_start + t > self.capacity:
             raise ValueError("KV cache capacity exceeded")
@@ -228,11 +277,15 @@ class FullAttentionLayer:
         if mode == "decode":
             if t != 1:
                 raise ValueError("decode takes one token")
-            # norm+rope writes K into the cache row; the decode core then needs no k_new.
-            q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
-                                        self.k_cache, self.v_cache, position_start)
-            gate = q_gate.view(HQ, 2 * HEAD_DIM)[:, HEAD_DIM:]
-            attn = _decode_with_strided_gate(q, self.k_cache, self.v_cache, cache_end, gate)
+            if fused:
+                attn = decode_step(q_gate, k, v, w["q_norm"], w["k_norm"], self.k_cache,
+                                   self.v_cache, position_start, cache_end)
+            else:
+                # norm+rope writes K into the cache row; the decode core then needs no k_new.
+                q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
+                                            self.k_cache, self.v_cache, position_start)
+                gate = q_gate.view(HQ, 2 * HEAD_DIM)[:, HEAD_DIM:]
+                attn = _decode_with_strided_gate(q, self.k_cache, self.v_cache, cache_end, gate)
         else:
             q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
                                         self.k_cache, self.v_cache, position_start)

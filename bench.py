@@ -173,6 +173,54 @@ def bench_decode(torch, fa, dev, cache_end, layers, iters, warmup, use_graph, se
             "frac_hbm": nbytes / (us_tok * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_decode_layer_step(torch, fa, dev, cache_end, layers, iters, warmup, use_graph,
+                            fused=True, seed=5):
+    """The full-attention part of a decode token between the projections and
+    o_proj, through ``layers`` layers at KV length ``cache_end``: head norm +
+    RoPE of q and the new k, the KV-row write, split-K attention and the
+    output gate -- fused into the decode launches (``fused``) or as the
+    separate head-norm/RoPE launch followed by the decode core."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    cap = cache_end
+    layer_t = []
+    for _ in range(layers):
+        k = torch.empty(cap, 2, 256, dtype=torch.bfloat16, device=dev)
+        v = torch.empty_like(k)
+        step = 16384
+        for s0 in range(0, cap, step):
+            n = min(step, cap - s0)
+            k[s0:s0 + n].copy_(torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16))
+            v[s0:s0 + n].copy_(torch.randn(n, 2, 256, generator=gen).to(torch.bfloat16))
+        layer_t.append(dict(
+            k=k, v=v, q_gate=torch.randn(1, 8192, generator=gen).to(torch.bfloat16).to(dev),
+            kr=torch.randn(1, 512, generator=gen).to(torch.bfloat16).to(dev),
+            vr=torch.randn(1, 512, generator=gen).to(torch.bfloat16).to(dev),
+            qn=(torch.randn(256, generator=gen) * 0.1).to(torch.bfloat16).to(dev),
+            kn=(torch.randn(256, generator=gen) * 0.1).to(torch.bfloat16).to(dev),
+            out=torch.empty(1, 4096, dtype=torch.bfloat16, device=dev),
+            q=torch.empty(1, 16, 256, dtype=torch.bfloat16, device=dev)))
+    pos = cache_end - 1
+
+    def step():
+        for d in layer_t:
+            if fused:
+                fa.decode_step(d["q_gate"], d["kr"], d["vr"], d["qn"], d["kn"], d["k"], d["v"],
+                               pos, cache_end, out=d["out"])
+            else:
+                fa.head_norm_rope_kv_write(d["q_gate"], d["kr"], d["vr"], d["qn"], d["kn"],
+                                           d["k"], d["v"], pos, q_out=d["q"])
+                fa.decode_gqa(d["q"], d["k"], d["v"], pos, cache_end,
+                              gate=d["q_gate"].view(16, 512)[:, 256:], out=d["out"])
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    nbytes = DECODE_BYTES_PER_TOKEN * cache_end * layers
+    del layer_t
+    return {"cache_end": cache_end, "layers": layers, "launches_per_layer": 2 if fused else 3,
+            "us_per_token": us, "hbm_gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def causal_pairs(t, s):
     off = s - t
     return t * off + t * (t + 1) // 2
@@ -355,6 +403,11 @@ def main():
         "decode_32k_1layer": bench_decode(torch, fa, dev, 32768, 1, 50, 5, use_graph),
         "decode_32k_10layers": bench_decode(torch, fa, dev, 32768, N_FULL_LAYERS, 20, 3, use_graph),
         "decode_262143": bench_decode(torch, fa, dev, 262143, N_FULL_LAYERS, 10, 2, use_graph),
+        "decode_layer_step_128k_fused": bench_decode_layer_step(torch, fa, dev, 131072, N_FULL_LAYERS,
+                                                               20, 3, use_graph),
+        "decode_layer_step_128k_unfused": bench_decode_layer_step(torch, fa, dev, 131072,
+                                                                 N_FULL_LAYERS, 20, 3, use_graph,
+                                                                 fused=False),
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),

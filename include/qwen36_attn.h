@@ -72,6 +72,27 @@ int qwen36_decode_gqa(const void* q, const void* k_new, const void* v_new,
                       size_t workspace_bytes, unsigned split_tokens,
                       void* stream);
 
+/* qwen36_decode_step: the whole one-token decode of a gated full-attention
+ * layer between its projections and o_proj, in one split launch plus the
+ * combine: head RMSNorm (w + 1) and partial RoPE of the 16 query heads and of
+ * the new key, the K (normalised) / V (raw) cache-row write at `position`,
+ * split-K attention over rows [0, cache_end) and the sigmoid output gate.
+ * Replaces the reference decode's norm/rope/KV-write launch plus its
+ * attention core (four_layer_mini_engine.py:933
+ * triton_full_attention_norm_rope_kv_write_kernel and :6614-6650;
+ * native_full_attention.hip.cpp:58-69, :681-765).
+ * q_gate: the q-projection row [16 x (256 query | 256 gate)] bf16; k_raw,
+ * v_raw: [2 x 256] bf16 before the head norm; q/k_norm_weight [256] bf16;
+ * caches [capacity, 2, 256] bf16; out [4096] bf16; workspace as for
+ * qwen36_decode_gqa (same size function).  Rounding is identical to
+ * qwen36_head_norm_rope followed by qwen36_decode_gqa. */
+int qwen36_decode_step(const void* q_gate, const void* k_raw, const void* v_raw,
+                       const void* q_norm_weight, const void* k_norm_weight,
+                       void* k_cache, void* v_cache, unsigned position,
+                       unsigned cache_end, unsigned capacity, void* out,
+                       void* workspace, size_t workspace_bytes,
+                       unsigned split_tokens, void* stream);
+
 /* ---- full-attention pointwise ----------------------------------------------
  * qwen36_rotary_table: replaces prefill_rotary_table_kernel /
  *   decode_rotary_kernel (native_pointwise.hip.cpp:224-238,

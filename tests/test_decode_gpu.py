@@ -100,3 +100,34 @@ def test_decode_rejects_bad_geometry(gpu):
     q, k, v = _inputs(64, seed=1)
     with pytest.raises(ValueError):
         decode_gqa(q.to(gpu), k.to(gpu), v.to(gpu), 0, 65)
+
+
+@pytest.mark.parametrize("cache_end,position,split_tokens", [
+    (1, 0, 0), (33, 32, 0), (1000, 999, 0), (4097, 4096, 0), (4096, 1234, 0),
+    (20000, 19999, 256), (131072, 131071, 0)])
+def test_decode_step_equals_norm_rope_then_decode(gpu, cache_end, position, split_tokens):
+    """The fused decode step (head norm + RoPE + KV-row write + attention +
+    gate in the split/combine launches) rounds exactly like the two-launch
+    path qwen36_head_norm_rope -> qwen36_decode_gqa: outputs and cache rows
+    are bit-identical."""
+    from qwen36_attn.full_attention import (decode_step, decode_gqa,
+                                            head_norm_rope_kv_write)
+    g = torch.Generator().manual_seed(cache_end + position)
+    cap = cache_end + 5
+    kc = torch.randn(cap, 2, 256, generator=g).to(torch.bfloat16).to(gpu)
+    vc = torch.randn(cap, 2, 256, generator=g).to(torch.bfloat16).to(gpu)
+    q_gate = (torch.randn(1, 8192, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    k = (torch.randn(1, 512, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    v = torch.randn(1, 512, generator=g).to(torch.bfloat16).to(gpu)
+    qn = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    kn = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16).to(gpu)
+    print(f"decode step S={cache_end} pos={position}", flush=True)
+    kc2, vc2 = kc.clone(), vc.clone()
+    fused = decode_step(q_gate, k, v, qn, kn, kc, vc, position, cache_end,
+                        split_tokens=split_tokens)
+    q = head_norm_rope_kv_write(q_gate, k, v, qn, kn, kc2, vc2, position)
+    gate = q_gate.view(16, 512)[:, 256:]
+    ref = decode_gqa(q, kc2, vc2, position, cache_end, gate=gate, split_tokens=split_tokens)
+    torch.cuda.synchronize()
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+    assert torch.equal(fused, ref)
