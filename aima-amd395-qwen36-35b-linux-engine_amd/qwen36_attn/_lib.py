@@ -16,6 +16,9 @@ _u32 = ctypes.c_uint
 _i32 = ctypes.c_int
 _sz = ctypes.c_size_t
 _f32 = ctypes.c_float
+_u64 = ctypes.c_ulonglong
+_pu32 = ctypes.POINTER(ctypes.c_uint)
+_pu64 = ctypes.POINTER(ctypes.c_ulonglong)
 
 # name -> (restype, argtypes).  Mirrors include/qwen36_attn.h.
 SIGNATURES: dict[str, tuple] = {
@@ -47,6 +50,16 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
                                         _vp, _vp, _vp, _u32, _vp, _sz, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
+    # exact-prefix cache
+    "qwen36_prefix_cache_create": (_vp, [_u32, _u64, _u32]),
+    "qwen36_prefix_cache_entries": (_u32, [_vp]),
+    "qwen36_prefix_cache_add_slice": (_i32, [_vp, _vp, _u64, _u64]),
+    "qwen36_prefix_cache_finalize": (_i32, [_vp, _pu64]),
+    "qwen36_prefix_cache_lookup": (_i32, [_vp, _pu32, _u32, _pu32, _pu32]),
+    "qwen36_prefix_cache_restore": (_i32, [_vp, _u32, _vp, _pu64]),
+    "qwen36_prefix_cache_capture": (_i32, [_vp, _pu32, _u32, _vp, _vp, _pu32, _pu64]),
+    "qwen36_prefix_cache_copy_terminal": (_i32, [_vp, _u32, _vp, _vp]),
+    "qwen36_prefix_cache_destroy": (_i32, [_vp]),
     "qwen36_gdn_decode_step": (_i32, [_vp, _u32, _vp, _vp, _vp, _vp, _vp, _u32, _vp,
                                       _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
 }

@@ -220,6 +220,18 @@ class LinearAttentionLayer:
         self.conv_state = torch.zeros(CONV_DIM, 3, dtype=torch.bfloat16, device=device)
         self.ssm_state = torch.zeros(HV, DK, DV, dtype=torch.float32, device=device)
         self.conv_spare = None   # second conv-state buffer for the fused decode step
+        self._conv_home = self.conv_state
+
+    def normalize_state(self) -> None:
+        """Keep the carried conv state in the buffer allocated at construction
+        (the fused decode step ping-pongs two buffers), as the reference's
+        normalize_linear_decode_state does before a prefix-cache capture
+        (native_resident_engine.hip.cpp:272-296): registered state pointers
+        stay valid."""
+        if self.conv_spare is not None and self.conv_state.data_ptr() != self._conv_home.data_ptr():
+            self._conv_home.copy_(self.conv_state)
+            self.conv_spare = self.conv_state
+            self.conv_state = self._conv_home
 
     def forward(self, inp: torch.Tensor, mode: str, fused: bool = True) -> torch.Tensor:
         """``mode == "decode"`` runs the fused one-launch step
@@ -250,6 +262,6 @@ class LinearAttentionLayer:
             new_state = torch.empty_like(self.ssm_state)
             core, _ = chunk_gated_delta_rule(q, k, v, g, beta, self.ssm_state,
                                              final_state=new_state)
-            self.ssm_state = new_state
+            self.ssm_state.copy_(new_state)   # keep the state buffer (prefix-cache slices)
         gated = gated_rmsnorm(core, z, w["norm"])
         return gated @ w["out_proj"].t()

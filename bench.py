@@ -221,6 +221,51 @@ def bench_decode_layer_step(torch, fa, dev, cache_end, layers, iters, warmup, us
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_prefix_cache(torch, dev, tokens, iters, warmup):
+    """Exact-prefix cache at model scale: the state of 10 full-attention
+    layers (K and V caches, capacity = ``tokens``) and 30 Gated-DeltaNet
+    layers (conv + recurrent state) captured for a ``tokens``-token prompt and
+    restored, each as one batched copy launch.  Bandwidth counts read + write
+    of the copied bytes."""
+    import ctypes
+    from qwen36_attn import _lib
+    lib = _lib.load(("qwen36_prefix_cache_create",))
+    pool = lib.qwen36_prefix_cache_create(tokens, 4096, 1)
+    bufs = []
+    for _ in range(N_FULL_LAYERS):
+        for _kv in range(2):
+            t = torch.empty(tokens, 2, 256, dtype=torch.bfloat16, device=dev)
+            bufs.append(t)
+            _lib.call("qwen36_prefix_cache_add_slice", pool, t.data_ptr(), t.numel() * 2, 1024)
+    for _ in range(GDN_LAYERS):
+        c = torch.empty(8192, 3, dtype=torch.bfloat16, device=dev)
+        s_ = torch.empty(32, 128, 128, dtype=torch.float32, device=dev)
+        bufs += [c, s_]
+        _lib.call("qwen36_prefix_cache_add_slice", pool, c.data_ptr(), c.numel() * 2, 0)
+        _lib.call("qwen36_prefix_cache_add_slice", pool, s_.data_ptr(), s_.numel() * 4, 0)
+    _lib.call("qwen36_prefix_cache_finalize", pool, None)
+    hidden = torch.empty(2048, dtype=torch.bfloat16, device=dev)
+    toks = (ctypes.c_uint * tokens)(*range(tokens))
+    st = torch.cuda.current_stream().cuda_stream
+    nbytes = ctypes.c_ulonglong(0)
+
+    def capture():
+        _lib.call("qwen36_prefix_cache_capture", pool, toks, tokens, hidden.data_ptr(), st,
+                  None, ctypes.byref(nbytes))
+
+    def restore():
+        _lib.call("qwen36_prefix_cache_restore", pool, 0, st, None)
+    t_cap = Timer(torch).time(capture, iters, warmup)
+    t_res = Timer(torch).time(restore, iters, warmup)
+    moved = nbytes.value
+    lib.qwen36_prefix_cache_destroy(pool)
+    del bufs
+    res = {"tokens": tokens, "bytes": moved, "capture_us": t_cap * 1e3, "restore_us": t_res * 1e3,
+           "restore_gbs_rw": 2 * moved / (t_res * 1e-3) / 1e9}
+    res["frac_hbm"] = res["restore_gbs_rw"] / HBM_PEAK_GBS
+    return res
+
+
 def causal_pairs(t, s):
     off = s - t
     return t * off + t * (t + 1) // 2
@@ -411,6 +456,7 @@ def main():
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
+        "prefix_cache_32k": bench_prefix_cache(torch, dev, 32768, 20, 3),
         "gdn_decode_step_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "gdn_decode_unfused_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5,
                                                              use_graph, fused=False),

@@ -188,6 +188,34 @@ int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
                            const void* state_in, void* state_out, void* out,
                            unsigned tokens, void* stream);
 
+/* ---- exact-prefix cache ----------------------------------------------------
+ * Replaces NativeExactPrefixCache and the resident engine's entry pool
+ * (native_resident_engine.hip.cpp:121-296, :553-560, :706-719, :826-836,
+ * :1197-1214).  A pool owns `entries` snapshots (0 = the reference's rule:
+ * 4 up to 32K tokens of capacity, 2 up to 128K, else 1).  Registered slices
+ * are live device buffers: per-token (bytes_per_token > 0, capacity ==
+ * max_tokens * bytes_per_token; a layer's K or V cache) or fixed (a GDN
+ * layer's conv / recurrent state).  Capture and restore are one batched copy
+ * launch each on the caller's stream; lookup is host-side (longest matching
+ * token prefix); capture fills the first empty entry, else the least
+ * recently used.  Pointers and sizes are 16-byte multiples.  create returns
+ * NULL on bad arguments; the others return 0 or a hipError_t value. */
+void* qwen36_prefix_cache_create(unsigned max_tokens, unsigned long long terminal_bytes,
+                                 unsigned entries);
+unsigned qwen36_prefix_cache_entries(void* pool);
+int qwen36_prefix_cache_add_slice(void* pool, void* live, unsigned long long capacity_bytes,
+                                  unsigned long long bytes_per_token);
+int qwen36_prefix_cache_finalize(void* pool, unsigned long long* bytes_out);
+int qwen36_prefix_cache_lookup(void* pool, const unsigned* tokens, unsigned n,
+                               unsigned* matched, unsigned* index);
+int qwen36_prefix_cache_restore(void* pool, unsigned index, void* stream,
+                                unsigned long long* bytes_out);
+int qwen36_prefix_cache_capture(void* pool, const unsigned* tokens, unsigned n,
+                                const void* terminal, void* stream, unsigned* index_out,
+                                unsigned long long* bytes_out);
+int qwen36_prefix_cache_copy_terminal(void* pool, unsigned index, void* dst, void* stream);
+int qwen36_prefix_cache_destroy(void* pool);
+
 #ifdef __cplusplus
 }
 #endif
