@@ -260,32 +260,44 @@ class FullAttentionLayer:
         self.capacity = capacity
         self.k_cache = torch.zeros(capacity, HKV, HEAD_DIM, dtype=torch.bfloat16, device=device)
         self.v_cache = torch.zeros_like(self.k_cache)
+        self._qkv = None   # fused decode projection, built on first use
 
     def forward(self, inp: torch.Tensor, position_start: int, mode: str,
                 fused: bool = True) -> torch.Tensor:
-        """``mode == "decode"`` runs the fused step (``decode_step``: norm,
-        RoPE, KV write, attention and gate in the split + combine launches)
-        unless ``fused`` is False (separate head-norm/RoPE launch)."""
+        """``mode == "decode"`` runs the native one-token path -- the fused
+        q|gate/k/v GEMV, the fused decode step (norm, RoPE, KV write,
+        attention and gate in the split + combine launches) and the o_proj
+        GEMV -- unless ``fused`` is False (torch projections, separate
+        head-norm/RoPE launch, decode core)."""
         t = inp.shape[0]
         if position_start + t > self.capacity:
             raise ValueError("KV cache capacity exceeded")
         w = self.w
+        cache_end = position_start + t
+        if mode == "decode" and fused:
+            # one token: the HIP GEMV for the fused q|gate, k, v projection and
+            # o_proj, the fused decode step in between
+            if t != 1:
+                raise ValueError("decode takes one token")
+            if self._qkv is None:
+                from .projections import FusedProjection
+                self._qkv = FusedProjection(w["q_proj"], w["k_proj"], w["v_proj"])
+            q_gate, k, v = self._qkv(inp)
+            attn = decode_step(q_gate, k, v, w["q_norm"], w["k_norm"], self.k_cache,
+                               self.v_cache, position_start, cache_end)
+            from .projections import gemv
+            return gemv(w["o_proj"], attn)
         q_gate = inp @ w["q_proj"].t()
         k = inp @ w["k_proj"].t()
         v = inp @ w["v_proj"].t()
-        cache_end = position_start + t
         if mode == "decode":
             if t != 1:
                 raise ValueError("decode takes one token")
-            if fused:
-                attn = decode_step(q_gate, k, v, w["q_norm"], w["k_norm"], self.k_cache,
-                                   self.v_cache, position_start, cache_end)
-            else:
-                # norm+rope writes K into the cache row; the decode core then needs no k_new.
-                q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
-                                            self.k_cache, self.v_cache, position_start)
-                gate = q_gate.view(HQ, 2 * HEAD_DIM)[:, HEAD_DIM:]
-                attn = _decode_with_strided_gate(q, self.k_cache, self.v_cache, cache_end, gate)
+            # norm+rope writes K into the cache row; the decode core then needs no k_new.
+            q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
+                                        self.k_cache, self.v_cache, position_start)
+            gate = q_gate.view(HQ, 2 * HEAD_DIM)[:, HEAD_DIM:]
+            attn = _decode_with_strided_gate(q, self.k_cache, self.v_cache, cache_end, gate)
         else:
             q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
                                         self.k_cache, self.v_cache, position_start)

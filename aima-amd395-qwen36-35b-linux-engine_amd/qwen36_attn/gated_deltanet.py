@@ -221,6 +221,7 @@ class LinearAttentionLayer:
         self.ssm_state = torch.zeros(HV, DK, DV, dtype=torch.float32, device=device)
         self.conv_spare = None   # second conv-state buffer for the fused decode step
         self._conv_home = self.conv_state
+        self._in_proj = None   # fused decode input projection, built on first use
 
     def normalize_state(self) -> None:
         """Keep the carried conv state in the buffer allocated at construction
@@ -234,10 +235,25 @@ class LinearAttentionLayer:
             self.conv_state = self._conv_home
 
     def forward(self, inp: torch.Tensor, mode: str, fused: bool = True) -> torch.Tensor:
-        """``mode == "decode"`` runs the fused one-launch step
-        (``gdn_decode_step``) unless ``fused`` is False, which runs the same
-        step as four launches (conv, gating, recurrent, gated norm)."""
+        """``mode == "decode"`` runs the native path -- for one token the
+        fused in-projection GEMV, the one-launch step (``gdn_decode_step``)
+        and the out_proj GEMV; for several tokens torch projections around the
+        same step -- unless ``fused`` is False, which runs torch projections
+        and the step as four launches (conv, gating, recurrent, gated norm)."""
         w = self.w
+        if mode == "decode" and fused and inp.shape[0] == 1:
+            # one token: the fused qkv|z|b|a GEMV, the fused step, the out_proj GEMV
+            from .projections import FusedProjection, gemv
+            if self._in_proj is None:
+                self._in_proj = FusedProjection(w["in_proj_qkv"], w["in_proj_z"],
+                                                w["in_proj_b"], w["in_proj_a"])
+            mixed, z, b, a = self._in_proj(inp)
+            if self.conv_spare is None:
+                self.conv_spare = torch.empty_like(self.conv_state)
+            gated = gdn_decode_step(mixed, self.conv_state, self.conv_spare, w["conv1d"], a, b,
+                                    w["A_log"], w["dt_bias"], z, w["norm"], self.ssm_state)
+            self.conv_state, self.conv_spare = self.conv_spare, self.conv_state
+            return gemv(w["out_proj"], gated)
         mixed = inp @ w["in_proj_qkv"].t()
         z = inp @ w["in_proj_z"].t()
         b = inp @ w["in_proj_b"].t()

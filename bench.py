@@ -266,6 +266,39 @@ def bench_prefix_cache(torch, dev, tokens, iters, warmup):
     return res
 
 
+def bench_decode_projections(torch, dev, iters, warmup, use_graph, native=True, seed=6):
+    """One decode token's projection GEMVs through the 40-layer stack: 10
+    full-attention layers (fused q|gate,k,v [9216,2048] + o_proj [2048,4096])
+    and 30 Gated-DeltaNet layers (fused qkv|z|b|a [12352,2048] + out_proj
+    [2048,4096]), distinct weights per layer (2.57 GB), with the HIP GEMV
+    (``native``) or torch.matmul."""
+    from qwen36_attn.projections import gemv
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    shapes = [(9216, 2048), (2048, 4096)] * N_FULL_LAYERS + [(12352, 2048), (2048, 4096)] * GDN_LAYERS
+    ws = []
+    for n, k in shapes:
+        w = torch.empty(n, k, dtype=torch.bfloat16, device=dev)
+        w.copy_((torch.randn(n, k, generator=gen) * 0.02).to(torch.bfloat16))
+        ws.append(w)
+    xs = {k: torch.randn(1, k, generator=gen).to(torch.bfloat16).to(dev) for k in (2048, 4096)}
+    outs = [torch.empty(1, n, dtype=torch.bfloat16, device=dev) for n, _ in shapes]
+
+    def step():
+        for w, o in zip(ws, outs):
+            x = xs[w.shape[1]]
+            if native:
+                gemv(w, x, out=o)
+            else:
+                torch.matmul(x, w.t(), out=o)
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    nbytes = sum(n * k * 2 for n, k in shapes)
+    del ws
+    return {"gemvs": len(shapes), "weight_bytes": nbytes, "us_per_token": us,
+            "hbm_gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def causal_pairs(t, s):
     off = s - t
     return t * off + t * (t + 1) // 2
@@ -457,6 +490,9 @@ def main():
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "prefix_cache_32k": bench_prefix_cache(torch, dev, 32768, 20, 3),
+        "decode_projections_40layers": bench_decode_projections(torch, dev, 20, 3, use_graph),
+        "decode_projections_40layers_torch": bench_decode_projections(torch, dev, 20, 3, use_graph,
+                                                                      native=False),
         "gdn_decode_step_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "gdn_decode_unfused_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5,
                                                              use_graph, fused=False),

@@ -188,6 +188,17 @@ int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
                            const void* state_in, void* state_out, void* out,
                            unsigned tokens, void* stream);
 
+/* ---- decode projections ----------------------------------------------------
+ * qwen36_gemv_bf16: y[N] = W[N,K] x[K] for one token, bf16 in and out with
+ * fp32 accumulation; replaces the decode projection GEMVs
+ * (native_full_layer.hip.cpp:154-174 fused q/k/v and o_proj,
+ * native_linear_layer.hip.cpp:151-157 in/out projections; torch form
+ * `inp @ W.t()` in four_layer_mini_engine.py:6566-6573, :6386-6395).
+ * W row-major [N, K] (out x in features), K = 2048 or 4096, W and x 16-byte
+ * aligned. */
+int qwen36_gemv_bf16(const void* w, unsigned n_rows, unsigned k, const void* x, void* y,
+                     void* stream);
+
 /* ---- exact-prefix cache ----------------------------------------------------
  * Replaces NativeExactPrefixCache and the resident engine's entry pool
  * (native_resident_engine.hip.cpp:121-296, :553-560, :706-719, :826-836,
