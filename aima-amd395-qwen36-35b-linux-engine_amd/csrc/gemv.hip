@@ -48,6 +48,7 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_bf16_kernel(
       for (int j = 0; j < kSteps; ++j)
         wr[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + 512 * j));
     }
+    __builtin_amdgcn_sched_barrier(0);   // keep every weight load in flight before the FMAs
     float acc[kGvRows];
 #pragma unroll
     for (int r = 0; r < kGvRows; ++r) {

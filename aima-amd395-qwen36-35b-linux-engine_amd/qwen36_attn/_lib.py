@@ -52,6 +52,9 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     # decode projections
     "qwen36_gemv_bf16": (_i32, [_vp, _u32, _u32, _vp, _vp, _vp]),
+    # MoE block
+    "qwen36_moe_decode_workspace_bytes": (_sz, []),
+    "qwen36_moe_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _sz, _vp]),
     # exact-prefix cache
     "qwen36_prefix_cache_create": (_vp, [_u32, _u64, _u32]),
     "qwen36_prefix_cache_entries": (_u32, [_vp]),

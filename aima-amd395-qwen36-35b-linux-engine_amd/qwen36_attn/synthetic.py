@@ -75,3 +75,20 @@ def causal_pairs(q_tokens: int, kv_tokens: int) -> int:
 
 def rope_inv_freq_reference() -> list[float]:
     return [1.0 / math.pow(1.0e7, 2.0 * i / 64.0) for i in range(32)]
+
+
+def moe_weights(g: torch.Generator, n_experts: int = 256, std: float = 0.02,
+                router_std: float = 0.05) -> dict:
+    """One MoE block (Qwen3.6-35B-A3B geometry: hidden 2048, expert and
+    shared intermediate 512, top-8), N(0, std) bf16; the post-attention norm
+    weight is N(0, 0.1) (it enters as w + 1)."""
+    return {
+        "post_attention_layernorm": randn((2048,), g, 0.1),
+        "router": randn((n_experts, 2048), g, router_std),
+        "expert_gate_up": randn((n_experts, 1024, 2048), g, std),
+        "expert_down": randn((n_experts, 2048, 512), g, std),
+        "shared_gate": randn((1, 2048), g, std),
+        "shared_gate_proj": randn((512, 2048), g, std),
+        "shared_up_proj": randn((512, 2048), g, std),
+        "shared_down_proj": randn((2048, 512), g, std),
+    }

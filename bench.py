@@ -299,6 +299,42 @@ def bench_decode_projections(torch, dev, iters, warmup, use_graph, native=True, 
             "hbm_gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_moe_decode(torch, dev, layers, iters, warmup, use_graph, seed=7):
+    """One decode token through the MoE blocks of ``layers`` layers (256
+    experts, top-8, intermediate 512, shared expert), distinct weights per
+    layer (1.5 GB each, generated on the device).  Bytes per layer-token =
+    router + shared input rows (1281 x 4 KiB) + 8 experts x 6 MiB + shared
+    down (2 MiB)."""
+    from qwen36_attn.moe import MoEBlock
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def rnd(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(torch.bfloat16)
+    blocks = []
+    for _ in range(layers):
+        w = {"post_attention_layernorm": rnd((2048,), 0.1), "router": rnd((256, 2048), 0.05),
+             "expert_gate_up": rnd((256, 1024, 2048), 0.02), "expert_down": rnd((256, 2048, 512), 0.02),
+             "shared_gate": rnd((1, 2048), 0.02), "shared_gate_proj": rnd((512, 2048), 0.02),
+             "shared_up_proj": rnd((512, 2048), 0.02), "shared_down_proj": rnd((2048, 512), 0.02)}
+        blocks.append(MoEBlock(w))
+    xs = [rnd((1, 2048), 0.5) for _ in range(layers)]
+    at = [rnd((1, 2048), 0.5) for _ in range(layers)]
+    outs = [torch.empty(1, 2048, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+
+    def step():
+        for b, x, a, o in zip(blocks, xs, at, outs):
+            b.decode(x, a, out=o)
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    per_layer = (256 + 1 + 1024) * 2048 * 2 + 8 * (1024 * 2048 + 2048 * 512) * 2 + 2048 * 512 * 2
+    nbytes = per_layer * layers
+    del blocks
+    torch.cuda.empty_cache()
+    return {"layers": layers, "bytes_per_token": nbytes, "us_per_token": us,
+            "hbm_gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def causal_pairs(t, s):
     off = s - t
     return t * off + t * (t + 1) // 2
@@ -491,6 +527,7 @@ def main():
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "prefix_cache_32k": bench_prefix_cache(torch, dev, 32768, 20, 3),
         "decode_projections_40layers": bench_decode_projections(torch, dev, 20, 3, use_graph),
+        "moe_decode_40layers": bench_moe_decode(torch, dev, 40, 20, 3, use_graph),
         "decode_projections_40layers_torch": bench_decode_projections(torch, dev, 20, 3, use_graph,
                                                                       native=False),
         "gdn_decode_step_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5, use_graph),

@@ -199,6 +199,27 @@ int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
 int qwen36_gemv_bf16(const void* w, unsigned n_rows, unsigned k, const void* x, void* y,
                      void* stream);
 
+/* ---- MoE block (one decode token) --------------------------------------------
+ * qwen36_moe_decode: the layer's step after attention for one token --
+ * residual add, post-attention RMSNorm (w + 1), router top-8 with softmax
+ * routing weights, the 8 routed experts (gate/up, SiLU, down) and the
+ * sigmoid-gated shared expert, summed into the residual -- with the bf16
+ * roundings of four_layer_mini_engine.py:8479-8650 (router :7775-7789,
+ * experts :7791-7803, shared :8240-8300); replaces the decode's router top-k
+ * kernels and native MoE consumer.  inp, attn_out, post_norm_w [2048] bf16;
+ * w_in [E+1+1024, 2048] = rows [router | shared_gate | shared gate_proj |
+ * shared up_proj]; expert_gate_up [E, 1024, 2048] (gate rows then up rows);
+ * expert_down [E, 2048, 512]; shared_down [2048, 512]; out [2048] bf16;
+ * 8 <= E <= 256, E % 4 == 0; all pointers 16-byte aligned; workspace of
+ * qwen36_moe_decode_workspace_bytes() bytes (holds the selected expert ids
+ * as int32 at byte offset 8192, their routing weights as fp32 at 8224 and
+ * the router logits as bf16 at 17472). */
+size_t qwen36_moe_decode_workspace_bytes(void);
+int qwen36_moe_decode(const void* inp, const void* attn_out, const void* post_norm_w,
+                      const void* w_in, const void* expert_gate_up, const void* expert_down,
+                      const void* shared_down, unsigned n_experts, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
 /* ---- exact-prefix cache ----------------------------------------------------
  * Replaces NativeExactPrefixCache and the resident engine's entry pool
  * (native_resident_engine.hip.cpp:121-296, :553-560, :706-719, :826-836,

@@ -344,3 +344,49 @@ def linear_attention(inp: torch.Tensor, weights: dict, conv_state: torch.Tensor,
         core, final = chunk_gated_delta_rule(*fn_args, chunk_size=chunk_size)
     gated = gated_rmsnorm(core.squeeze(0), z, weights["norm"])
     return gated @ weights["out_proj"].t(), new_conv, final.squeeze(0)
+
+
+# ---------------------------------------------------------------------------
+# MoE block after attention (four_layer_mini_engine.py:8479-8650)
+# ---------------------------------------------------------------------------
+MOE_TOP_K = 8
+
+
+def layer_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """fle:5127-5128 -- the layer RMSNorm: fp32 mean of squares, rsqrt,
+    weight + 1, rounded to bf16."""
+    variance = x.float().pow(2).mean(dim=-1, keepdim=True)
+    return (x.float() * torch.rsqrt(variance + eps) * (weight.float() + 1.0)).to(DTYPE)
+
+
+def moe_block(inp: torch.Tensor, attn_out: torch.Tensor, weights: dict,
+              forced_ids: torch.Tensor | None = None) -> torch.Tensor:
+    """fle:8479-8490 residual + post-attention norm, fle:7775-7789 router
+    (top-8 of the fp32 bf16 logits, softmax over the 8 -> bf16), fle:7791-7803
+    routed experts ("expanded" form), fle:8240-8300 shared expert, fle:8636-8640
+    sums.  inp, attn_out [T, 2048] bf16; returns [T, 2048] bf16.
+    ``forced_ids`` [T, 8] replaces torch.topk's selection (for tied logits)."""
+    after = inp + attn_out
+    h2 = layer_rmsnorm(after, weights["post_attention_layernorm"])
+    t = h2.shape[0]
+    logits = h2 @ weights["router"].t()
+    scores, ids = torch.topk(logits.float(), k=MOE_TOP_K, dim=-1)
+    if forced_ids is not None:
+        ids = forced_ids.long().view(t, MOE_TOP_K)
+        scores = logits.float().gather(-1, ids)
+    rw = torch.softmax(scores, dim=-1).to(DTYPE)
+    expanded = h2.repeat_interleave(MOE_TOP_K, dim=0)
+    flat = ids.reshape(-1)
+    gate_up = weights["expert_gate_up"][flat].transpose(1, 2)
+    projected = torch.bmm(expanded.unsqueeze(1), gate_up).squeeze(1)
+    gate, up = projected.chunk(2, dim=-1)
+    act = (F.silu(gate.float()) * up.float()).to(DTYPE)
+    down = weights["expert_down"][flat].transpose(1, 2)
+    y = torch.bmm(act.unsqueeze(1), down).squeeze(1)
+    moe = (y.view(t, MOE_TOP_K, -1) * rw.unsqueeze(-1)).sum(dim=1)
+    sg = h2 @ weights["shared_gate"].t()
+    sgp = h2 @ weights["shared_gate_proj"].t()
+    sup = h2 @ weights["shared_up_proj"].t()
+    sact = (F.silu(sgp.float()) * sup.float()).to(DTYPE)
+    shared = torch.sigmoid(sg).to(DTYPE) * (sact @ weights["shared_down_proj"].t())
+    return after + (moe + shared)

@@ -281,3 +281,44 @@ def test_full_attention_prefill_decode_consistency():
     last = O.full_attention(x[8:], w, kc2, vc2, 8, "decode")
     assert (last.float() - full[8:].float()).abs().max() <= 2e-2
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+
+
+def test_moe_block_matches_fp64_per_expert_loop():
+    """Pins oracle.moe_block (fle:7775-7803, 8240-8300, 8479-8640) with an fp64
+    brute force written from the definitions: gate = first 512 rows of an
+    expert's gate_up, up = the last 512, SiLU on the gate, routing weights =
+    softmax over the 8 largest router logits, shared expert scaled by the
+    sigmoid of its gate row, all added to the residual."""
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(31)
+    w = syn.moe_weights(g, n_experts=16)
+    inp = syn.randn((2, 2048), g, 0.5)
+    attn = syn.randn((2, 2048), g, 0.5)
+    got = O.moe_block(inp, attn, w).double()
+    after = (inp.double() + attn.double())
+    for t in range(2):
+        a = after[t]
+        h = a / torch.sqrt((a * a).mean() + 1e-6) * (w["post_attention_layernorm"].double() + 1)
+        logits = w["router"].double() @ h
+        top = torch.argsort(logits, descending=True)[:8]
+        rw = torch.softmax(logits[top], dim=0)
+        acc = torch.zeros(2048, dtype=torch.float64)
+        for e, r in zip(top.tolist(), rw.tolist()):
+            gu = w["expert_gate_up"][e].double() @ h
+            act = torch.nn.functional.silu(gu[:512]) * gu[512:]
+            acc += r * (w["expert_down"][e].double() @ act)
+        sg = torch.sigmoid(w["shared_gate"].double() @ h)
+        sact = torch.nn.functional.silu(w["shared_gate_proj"].double() @ h) * (w["shared_up_proj"].double() @ h)
+        ref = a + acc + sg * (w["shared_down_proj"].double() @ sact)
+        assert (got[t] - ref).abs().max().item() <= 2e-2 * max(1.0, ref.abs().max().item() / 8)
+
+
+def test_moe_block_forced_ids_equal_topk():
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(32)
+    w = syn.moe_weights(g, n_experts=12)
+    inp = syn.randn((3, 2048), g, 0.5)
+    attn = syn.randn((3, 2048), g, 0.5)
+    h2 = O.layer_rmsnorm(inp + attn, w["post_attention_layernorm"])
+    ids = torch.topk((h2 @ w["router"].t()).float(), 8, dim=-1).indices
+    assert torch.equal(O.moe_block(inp, attn, w), O.moe_block(inp, attn, w, forced_ids=ids))
