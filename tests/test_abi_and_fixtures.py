@@ -90,6 +90,49 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert step(zs=100) == 1
     assert step(abs_=8) == 1
     assert step(t=0) == 1
+    # fused full-attention decode step: nulls, position outside the cache
+    assert L.qwen36_decode_step(None, 16, 16, 16, 16, 16, 16, 0, 1, 1, 16, 16, 1 << 20, 0, None) == 1
+    assert L.qwen36_decode_step(16, 16, 16, 16, 16, 16, 16, 5, 5, 8, 16, 16, 1 << 20, 0, None) == 1
+    assert L.qwen36_decode_step(16, 16, 16, 16, 16, 16, 16, 0, 9, 8, 16, 16, 1 << 20, 0, None) == 1
+    # GEMV: K other than 2048/4096, zero rows, misaligned weights
+    assert L.qwen36_gemv_bf16(16, 4, 1024, 16, 16, None) == 1
+    assert L.qwen36_gemv_bf16(16, 0, 2048, 16, 16, None) == 1
+    assert L.qwen36_gemv_bf16(18, 4, 2048, 16, 16, None) == 1
+    # MoE decode: expert count out of range / not a multiple of 4, small workspace
+    ws = L.qwen36_moe_decode_workspace_bytes()
+    assert ws > 0
+    assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 4, 16, 16, ws, None) == 1
+    assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 257, 16, 16, ws, None) == 1
+    assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 30, 16, 16, ws, None) == 1
+    assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 32, 16, 16, ws - 1, None) == 1
+
+
+def test_prefix_cache_host_bookkeeping_without_device(lib):
+    """Pool creation rules and slice validation (no device memory is
+    touched before finalize): the reference's 4 / 2 / 1 entry rule
+    (native_resident_engine.hip.cpp:553-556), per-token slices must span
+    max_tokens rows, 16-byte alignment, lookups on an empty pool miss."""
+    import ctypes
+    from qwen36_attn import _lib
+    L = _lib.load()
+    assert not L.qwen36_prefix_cache_create(0, 4096, 0)
+    assert not L.qwen36_prefix_cache_create(1024, 4095, 0)
+    for cap, n in ((1024, 4), (32768, 4), (32769, 2), (131072, 2), (131073, 1), (262144, 1)):
+        p = L.qwen36_prefix_cache_create(cap, 4096, 0)
+        assert p and L.qwen36_prefix_cache_entries(p) == n
+        assert L.qwen36_prefix_cache_destroy(p) == 0
+    p = L.qwen36_prefix_cache_create(100, 4096, 3)
+    assert L.qwen36_prefix_cache_entries(p) == 3
+    assert L.qwen36_prefix_cache_add_slice(p, 4096, 100 * 1024, 1024) == 0
+    assert L.qwen36_prefix_cache_add_slice(p, 4096, 99 * 1024, 1024) == 1    # not max_tokens rows
+    assert L.qwen36_prefix_cache_add_slice(p, 4100, 4096, 0) == 1            # misaligned
+    assert L.qwen36_prefix_cache_add_slice(p, 4096, 4001, 0) == 1            # size not 16-byte multiple
+    toks = (ctypes.c_uint * 3)(1, 2, 3)
+    m, i = ctypes.c_uint(9), ctypes.c_uint(9)
+    assert L.qwen36_prefix_cache_lookup(p, toks, 3, ctypes.byref(m), ctypes.byref(i)) == 0
+    assert (m.value, i.value) == (0, 3)
+    assert L.qwen36_prefix_cache_restore(p, 0, None, None) == 1                # not finalized
+    assert L.qwen36_prefix_cache_destroy(p) == 0
 
 
 def test_fixtures_match_oracle():
