@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     const bf16* __restrict__ q, bf16* __restrict__ k_cache,
     bf16* __restrict__ v_cache, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
-    unsigned split_tokens, unsigned nsplit, DecodeWs ws, FuseArgs fz) {
+    unsigned nsplit, DecodeWs ws, FuseArgs fz) {
   __shared__ __attribute__((aligned(16))) char lds[kDecLds];
   const int kvh = blockIdx.y;
   const unsigned split = blockIdx.x;
@@ -96,7 +96,6 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // each row at about the same time), which keeps HBM pages and channels
   // evenly and sequentially used.
   const unsigned end = cache_end;
-  (void)split_tokens;
   // The workgroup that owns the new row's block writes it to the cache (this
   // KV head's half) and reads K/V for that token from k_new/v_new directly,
   // so no other workgroup depends on the write.
@@ -482,8 +481,8 @@ static int launch_decode(bool fuse, const void* q, const void* k_new,
   hipLaunchKernelGGL(kernel, dim3(nsplit, kHkv), dim3(256), 0, st,
                      static_cast<const bf16*>(q), static_cast<bf16*>(k_cache),
                      static_cast<bf16*>(v_cache), static_cast<const bf16*>(k_new),
-                     static_cast<const bf16*>(v_new), position, cache_end, per,
-                     nsplit, ws, fz);
+                     static_cast<const bf16*>(v_new), position, cache_end, nsplit, ws,
+                     fz);
   hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / kCombineDims), dim3(256),
                      0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
                      gate_head_stride, static_cast<bf16*>(out));
