@@ -30,16 +30,10 @@
 //     (0, 0) stores the ids and routing weights.
 //  3. moe_down_kernel: each wave owns 2 output rows and reads those rows of
 //     the 8 selected down matrices and the shared one, then combines.
-#include "common.h"
+#include "moe_common.h"
 
 namespace q36 {
 namespace {
-
-constexpr int kMoeHidden = 2048;
-constexpr int kMoeInter = 512;          // expert and shared intermediate size
-constexpr int kMoeTopK = 8;
-constexpr int kMoeMaxExperts = 256;
-constexpr float kMoeEps = 1e-6f;
 
 // Workspace layout (bytes).
 constexpr size_t kWsAfter = 0;                                   // bf16 [2048]
@@ -49,8 +43,6 @@ constexpr size_t kWsRw = kWsIds + kMoeTopK * 4;                   // float [8] (
 constexpr size_t kWsAct = kWsRw + kMoeTopK * 4;                   // bf16 [9][512]
 constexpr size_t kWsProj = kWsAct + (kMoeTopK + 1) * kMoeInter * 2;   // bf16 [E + 1 + 1024]
 constexpr size_t kWsBytes = kWsProj + (kMoeMaxExperts + 1 + 2 * kMoeInter) * 2;
-
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
 // GEMV of one row r (K = 2048) with x held as lane l's columns 8l + 512j.
 __device__ __forceinline__ float dot2048(const u32x4 (&wr)[4], const float (&xv)[4][8]) {
@@ -62,12 +54,6 @@ __device__ __forceinline__ float dot2048(const u32x4 (&wr)[4], const float (&xv)
     for (int e = 0; e < 8; ++e) a = __builtin_fmaf(bf2f(v[e]), xv[j][e], a);
   }
   return a;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
 }
 
 // ---- 1. residual + RMSNorm + fused router / shared-input GEMV -------------
@@ -137,55 +123,6 @@ __global__ __launch_bounds__(256, 2) void moe_router_kernel(
   }
 }
 
-// Max of a 32-bit unsigned key over the wave, result in every lane: DPP
-// within rows of 16 (quad perms, half mirror, mirror), then the row-pair and
-// half swaps of v_permlane16/32_swap -- no LDS round trips.
-__device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
-  v = max(v, (unsigned)__builtin_amdgcn_update_dpp((int)v, (int)v, 0xB1, 0xF, 0xF, false));  // quad xor 1
-  v = max(v, (unsigned)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x4E, 0xF, 0xF, false));  // quad xor 2
-  v = max(v, (unsigned)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x141, 0xF, 0xF, false)); // half mirror
-  v = max(v, (unsigned)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x140, 0xF, 0xF, false)); // mirror
-  const auto r16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  v = max((unsigned)r16[0], (unsigned)r16[1]);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  return max((unsigned)r32[0], (unsigned)r32[1]);
-}
-
-// Top-8 of the E router logits, ties to the lower expert index, by one wave:
-// a bf16 logit maps to an order-preserving 16-bit key (sign set: all bits
-// flipped; else sign bit set), packed above 0xFFFF - expert so one unsigned
-// max picks the largest logit and, among equal ones, the lowest expert.
-// Lane l holds experts l + 64i.  (-0 ranks below +0; NaN logits unsupported.)
-__device__ void select_top8(const bf16* __restrict__ logits, unsigned n_experts,
-                            int (&ids)[kMoeTopK], float (&vals)[kMoeTopK]) {
-  const int lane = threadIdx.x & 63;
-  unsigned key[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const unsigned e = lane + 64 * i;
-    unsigned k = 0;
-    if (e < n_experts) {
-      const unsigned b = __builtin_bit_cast(unsigned short, logits[e]);
-      const unsigned ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-      k = (ord << 16) | (0xFFFFu - e);
-    }
-    key[i] = k;
-  }
-#pragma unroll
-  for (int r = 0; r < kMoeTopK; ++r) {
-    unsigned best = max(max(key[0], key[1]), max(key[2], key[3]));
-    best = wave_max_u32(best);
-    const unsigned e = 0xFFFFu - (best & 0xFFFFu);
-    const unsigned ord = best >> 16;
-    const unsigned b = (ord & 0x8000u) ? (ord & 0x7FFFu) : (~ord & 0xFFFFu);
-    ids[r] = (int)e;
-    vals[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)b));
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (key[i] == best) key[i] = 0u;
-  }
-}
-
 // ---- 2. expert gate/up + SiLU ---------------------------------------------
 // grid = (9, 32); block = 256: wave w computes act rows tile*16 + 4w .. +4 of
 // slot blockIdx.x (its 4 gate rows and 4 up rows, 8 rows x 4 KiB in flight).
@@ -209,17 +146,12 @@ __global__ __launch_bounds__(256, 2) void moe_expert_up_kernel(
   float vals[kMoeTopK];
   select_top8(proj, n_experts, ids, vals);
   if (blockIdx.y == 0 && slot == 0 && wave == 0 && lane == 0) {
-    // routing weights: bf16(softmax over the 8 selected logits)
-    float mx = vals[0], sum = 0.f, ex[kMoeTopK];
-#pragma unroll
-    for (int k = 0; k < kMoeTopK; ++k) {
-      ex[k] = expf(vals[k] - mx);
-      sum += ex[k];
-    }
+    float rw[kMoeTopK];
+    routing_weights(vals, rw);
 #pragma unroll
     for (int k = 0; k < kMoeTopK; ++k) {
       reinterpret_cast<int*>(ws + kWsIds)[k] = ids[k];
-      reinterpret_cast<float*>(ws + kWsRw)[k] = bf2f(f2bf(ex[k] / sum));
+      reinterpret_cast<float*>(ws + kWsRw)[k] = rw[k];
     }
   }
   int e = ids[0];

@@ -55,6 +55,9 @@ SIGNATURES: dict[str, tuple] = {
     # MoE block
     "qwen36_moe_decode_workspace_bytes": (_sz, []),
     "qwen36_moe_decode": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp, _sz, _vp]),
+    "qwen36_moe_prefill_workspace_bytes": (_sz, [_u32, _u32]),
+    "qwen36_moe_prefill": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _vp, _vp, _sz,
+                                  _vp]),
     # exact-prefix cache
     "qwen36_prefix_cache_create": (_vp, [_u32, _u64, _u32]),
     "qwen36_prefix_cache_entries": (_u32, [_vp]),

@@ -60,3 +60,45 @@ class MoEBlock:
         rw = ws[WS_RW:WS_RW + 4 * TOP_K].view(torch.float32).clone()
         logits = ws[WS_LOGITS:WS_LOGITS + 2 * self.n_experts].view(torch.bfloat16).clone()
         return out, ids, rw, logits
+
+    def prefill(self, inp: torch.Tensor, attn_out: torch.Tensor,
+                out: torch.Tensor | None = None, debug: bool = False):
+        """T tokens (``qwen36_moe_prefill``): returns after + MoE(rmsnorm(after))
+        [T, 2048] bf16 with after = inp + attn_out.  ``debug`` also returns
+        (expert ids [T, 8] int32, routing weights [T, 8] fp32, router logits
+        [T, E] bf16, shared-gate logits [T] bf16) read back from the
+        workspace."""
+        for name, x in (("inp", inp), ("attn_out", attn_out)):
+            require(x, name, torch.bfloat16)
+            if x.dim() != 2 or x.shape[1] != HIDDEN:
+                raise ValueError(f"{name} must be [T, 2048]")
+        t = inp.shape[0]
+        if attn_out.shape[0] != t or t == 0:
+            raise ValueError("inp and attn_out must hold the same T >= 1 rows")
+        dev = inp.device
+        if out is None:
+            out = torch.empty(t, HIDDEN, dtype=torch.bfloat16, device=dev)
+        lib = _lib.load(("qwen36_moe_prefill", "qwen36_moe_prefill_workspace_bytes"))
+        nb = lib.qwen36_moe_prefill_workspace_bytes(t, self.n_experts)
+        if nb == 0:
+            raise ValueError("unsupported token count or expert count")
+        ws = scratch("moe_prefill", nb, dev)
+        w = self.w
+        _lib.call("qwen36_moe_prefill", ptr(inp), ptr(attn_out), ptr(w["post_attention_layernorm"]),
+                  ptr(self.w_in), ptr(w["expert_gate_up"]), ptr(w["expert_down"]),
+                  ptr(w["shared_down_proj"]), self.n_experts, t, ptr(out), ptr(ws), ws.numel(),
+                  stream_handle(dev))
+        if not debug:
+            return out
+
+        def region(offset, nbytes):
+            return ws[offset:offset + nbytes], (offset + nbytes + 255) // 256 * 256
+
+        ld = (self.n_experts + 8) & ~7
+        ids, o = region(0, 4 * TOP_K * t)
+        rw, o = region(o, 4 * TOP_K * t)
+        logits, _ = region(o, 2 * ld * t)
+        ids = ids.view(torch.int32).view(t, TOP_K).clone()
+        rw = rw.view(torch.float32).view(t, TOP_K).clone()
+        logits = logits.view(torch.bfloat16).view(t, ld)
+        return out, ids, rw, logits[:, :self.n_experts].clone(), logits[:, self.n_experts].clone()

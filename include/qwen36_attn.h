@@ -220,6 +220,26 @@ int qwen36_moe_decode(const void* inp, const void* attn_out, const void* post_no
                       const void* shared_down, unsigned n_experts, void* out, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/* ---- MoE block (prefill, T tokens) ------------------------------------------
+ * qwen36_moe_prefill: the same block for T = `tokens` rows (inp, attn_out,
+ * out [T, 2048] bf16), weights as for qwen36_moe_decode; replaces the
+ * reference's native MoE prefill (native_moe_prefill.hip.cpp: router GEMM and
+ * router_topk8_softmax_256_kernel :234-323, moe_align_block32_256_kernel
+ * :325-382, the two AOT fused_moe expert GEMMs with
+ * expert_silu_multiply_kernel :384-402, the shared-expert GEMMs and kernels
+ * :210-232, moe_sum8_kernel :404-430, the residual add) with the eager
+ * arithmetic of four_layer_mini_engine.py:8479-8650.  1 <= T <= 262144;
+ * workspace of qwen36_moe_prefill_workspace_bytes(T, E) bytes (0 = invalid
+ * arguments), which starts with the expert ids (int32 [T, 8]) at offset 0,
+ * the routing weights (fp32 [T, 8]) and the router logits (bf16 [T, ld],
+ * ld = (E + 8) & ~7, column E = the shared gate), each region 256-byte
+ * aligned. */
+size_t qwen36_moe_prefill_workspace_bytes(unsigned tokens, unsigned n_experts);
+int qwen36_moe_prefill(const void* inp, const void* attn_out, const void* post_norm_w,
+                       const void* w_in, const void* expert_gate_up, const void* expert_down,
+                       const void* shared_down, unsigned n_experts, unsigned tokens, void* out,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- exact-prefix cache ----------------------------------------------------
  * Replaces NativeExactPrefixCache and the resident engine's entry pool
  * (native_resident_engine.hip.cpp:121-296, :553-560, :706-719, :826-836,

@@ -360,12 +360,17 @@ def layer_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> t
 
 
 def moe_block(inp: torch.Tensor, attn_out: torch.Tensor, weights: dict,
-              forced_ids: torch.Tensor | None = None) -> torch.Tensor:
+              forced_ids: torch.Tensor | None = None, grouped: bool = False) -> torch.Tensor:
     """fle:8479-8490 residual + post-attention norm, fle:7775-7789 router
     (top-8 of the fp32 bf16 logits, softmax over the 8 -> bf16), fle:7791-7803
     routed experts ("expanded" form), fle:8240-8300 shared expert, fle:8636-8640
     sums.  inp, attn_out [T, 2048] bf16; returns [T, 2048] bf16.
-    ``forced_ids`` [T, 8] replaces torch.topk's selection (for tied logits)."""
+    ``forced_ids`` [T, 8] replaces torch.topk's selection (for tied logits).
+    ``grouped`` evaluates the routed experts one expert at a time (the rows
+    routed to expert e times its weights, as the reference's prefill groups
+    them, native_moe_prefill.hip.cpp:325-382) instead of gathering one weight
+    matrix per (token, rank): the same per-row products, with memory that does
+    not grow with T."""
     after = inp + attn_out
     h2 = layer_rmsnorm(after, weights["post_attention_layernorm"])
     t = h2.shape[0]
@@ -375,14 +380,23 @@ def moe_block(inp: torch.Tensor, attn_out: torch.Tensor, weights: dict,
         ids = forced_ids.long().view(t, MOE_TOP_K)
         scores = logits.float().gather(-1, ids)
     rw = torch.softmax(scores, dim=-1).to(DTYPE)
-    expanded = h2.repeat_interleave(MOE_TOP_K, dim=0)
     flat = ids.reshape(-1)
-    gate_up = weights["expert_gate_up"][flat].transpose(1, 2)
-    projected = torch.bmm(expanded.unsqueeze(1), gate_up).squeeze(1)
-    gate, up = projected.chunk(2, dim=-1)
-    act = (F.silu(gate.float()) * up.float()).to(DTYPE)
-    down = weights["expert_down"][flat].transpose(1, 2)
-    y = torch.bmm(act.unsqueeze(1), down).squeeze(1)
+    if grouped:
+        y = torch.empty(flat.numel(), h2.shape[1], dtype=DTYPE)
+        for e in flat.unique().tolist():
+            rows = (flat == e).nonzero().squeeze(1)
+            projected = h2[rows // MOE_TOP_K] @ weights["expert_gate_up"][e].t()
+            gate, up = projected.chunk(2, dim=-1)
+            act = (F.silu(gate.float()) * up.float()).to(DTYPE)
+            y[rows] = act @ weights["expert_down"][e].t()
+    else:
+        expanded = h2.repeat_interleave(MOE_TOP_K, dim=0)
+        gate_up = weights["expert_gate_up"][flat].transpose(1, 2)
+        projected = torch.bmm(expanded.unsqueeze(1), gate_up).squeeze(1)
+        gate, up = projected.chunk(2, dim=-1)
+        act = (F.silu(gate.float()) * up.float()).to(DTYPE)
+        down = weights["expert_down"][flat].transpose(1, 2)
+        y = torch.bmm(act.unsqueeze(1), down).squeeze(1)
     moe = (y.view(t, MOE_TOP_K, -1) * rw.unsqueeze(-1)).sum(dim=1)
     sg = h2 @ weights["shared_gate"].t()
     sgp = h2 @ weights["shared_gate_proj"].t()

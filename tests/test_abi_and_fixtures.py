@@ -105,6 +105,16 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 257, 16, 16, ws, None) == 1
     assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 30, 16, 16, ws, None) == 1
     assert L.qwen36_moe_decode(16, 16, 16, 16, 16, 16, 16, 32, 16, 16, ws - 1, None) == 1
+    # MoE prefill: token count 0 / above 262144, expert count out of range or
+    # not a multiple of 4, small workspace, misaligned output
+    W = L.qwen36_moe_prefill_workspace_bytes
+    assert W(0, 256) == 0 and W(262145, 256) == 0
+    assert W(16, 4) == 0 and W(16, 258) == 0 and W(16, 30) == 0
+    ws = W(16, 256)
+    assert ws > 0 and W(32, 256) > ws
+    assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 0, 16, 16, ws, None) == 1
+    assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 16, 16, 16, ws - 1, None) == 1
+    assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 16, 18, 16, ws, None) == 1
 
 
 def test_prefix_cache_host_bookkeeping_without_device(lib):

@@ -295,6 +295,7 @@ def test_moe_block_matches_fp64_per_expert_loop():
     inp = syn.randn((2, 2048), g, 0.5)
     attn = syn.randn((2, 2048), g, 0.5)
     got = O.moe_block(inp, attn, w).double()
+    got_grouped = O.moe_block(inp, attn, w, grouped=True).double()
     after = (inp.double() + attn.double())
     for t in range(2):
         a = after[t]
@@ -311,6 +312,21 @@ def test_moe_block_matches_fp64_per_expert_loop():
         sact = torch.nn.functional.silu(w["shared_gate_proj"].double() @ h) * (w["shared_up_proj"].double() @ h)
         ref = a + acc + sg * (w["shared_down_proj"].double() @ sact)
         assert (got[t] - ref).abs().max().item() <= 2e-2 * max(1.0, ref.abs().max().item() / 8)
+        assert (got_grouped[t] - ref).abs().max().item() <= 2e-2 * max(1.0, ref.abs().max().item() / 8)
+
+
+def test_moe_block_grouped_equals_expanded():
+    """The per-expert evaluation (prefill grouping) and the per-(token, rank)
+    expanded form compute the same rows: 6 tokens over 8 experts, so every
+    expert serves several rows."""
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(33)
+    w = syn.moe_weights(g, n_experts=8)
+    inp = syn.randn((6, 2048), g, 0.5)
+    attn = syn.randn((6, 2048), g, 0.5)
+    a = O.moe_block(inp, attn, w).float()
+    b = O.moe_block(inp, attn, w, grouped=True).float()
+    assert (a - b).abs().max().item() <= 1e-2
 
 
 def test_moe_block_forced_ids_equal_topk():
