@@ -23,7 +23,8 @@
 //  2. moe_gemm<kRouter>    logits [T, E + 1] = h2 [router | shared_gate]^T.
 //  3. moe_topk_kernel      top-8 + routing softmax + shared gate, a wave per token.
 //  4. moe_align_kernel     (token, rank) slots sorted by expert, each group
-//                          padded to 64-row tiles; one workgroup.
+//                          padded to 32 rows and cut into tiles of up to 256
+//                          rows; one workgroup.
 //  5. moe_gemm<kGateUp>    act [tile rows, 512] = silu(gate) * up per tile,
 //                          gate and up columns of one group in one workgroup.
 //  6. moe_gemm<kDown>      y rows scaled by their routing weight, scattered to
@@ -31,27 +32,49 @@
 //  7. moe_combine_kernel   per token: sum of the 8 routed rows, + shared, +
 //                          after.
 //
-// Grouped GEMM (MFMA-bound at large T; HBM-bound on the expert weights at
-// small T): workgroup tile 64 rows x 128 weight rows x 64 of K, 4 waves of
-// 32 x 64 on v_mfma_f32_32x32x16_bf16.  Both operands are K-contiguous in
-// memory, so tiles are fetched straight into LDS (buffer_load ... lds, 16
-// bytes per lane, 8 rows of 128 bytes per instruction) with an XOR swizzle
-// of the 16-byte chunks (chunk c of row r sits at c ^ (r & 7)) chosen by each
-// lane's source address, which makes the ds_read_b128 operand reads
-// conflict-free.  Double-buffered: the next K step's fetch is in flight
-// during the current step's MFMAs.  Work items (tile, column block) are dealt
-// to the 8 XCDs in contiguous ranges, so the tiles of one expert share an L2.
+// Grouped GEMM: a workgroup computes one tile of up to 128 rows of one
+// group against 256 weight rows, K in steps of 32, with 8 waves of 64 x 64 on
+// v_mfma_f32_32x32x16_bf16 (one 16-byte LDS read per MFMA); 32-row blocks past
+// the tile's rows are neither computed nor fetched.  Both operands are
+// K-contiguous in memory, so they are fetched straight into LDS
+// (buffer_load ... lds, 16 bytes per lane, 1 KiB per instruction) with an XOR
+// swizzle of the 16-byte chunks chosen by each lane's source address, which
+// makes the ds_read_b128 operand reads bank-conflict-free.  A 3-stage ring,
+// two workgroups per CU; the fetch is issued through inline asm (the
+// compiler would otherwise wait for it before reading the current stage) and
+// ordered by explicit vmcnt waits + barriers.  Work items (tile, column block)
+// are dealt to the 8 XCDs in contiguous ranges, so a tile's column blocks
+// and an expert's tiles share an L2.  Measured on MI355X: the loop is bound
+// by the L2/MALL -> LDS fill rate (~20-30 B/clk per CU), at ~87 flop per
+// fetched byte for this tile; the tile shape was chosen from a sweep of
+// 64..256-row x 128..256-column tiles, K steps of 32/64 and 2..4 stages.
 #include "moe_common.h"
 
 namespace q36 {
 namespace {
 
-constexpr int kPfBM = 64;                 // rows per tile
-constexpr int kPfBN = 128;                // weight rows per workgroup
-constexpr int kPfBK = 64;                 // K per step (128 bytes per row)
-constexpr int kPfRowB = kPfBK * 2;        // 128
-constexpr int kPfAStage = kPfBM * kPfRowB;        // 8192
-constexpr int kPfStage = kPfAStage + kPfBN * kPfRowB;   // 24576
+constexpr int kPfBM = 128;                // rows per tile (at most)
+constexpr int kPfPad = 32;                // group padding (rows)
+constexpr int kPfBN = 256;                // weight rows per workgroup
+constexpr int kPfWR = 64;                 // rows per wave (32-row blocks: kPfWR / 32)
+constexpr int kPfStages = 3;              // fetch ring depth
+constexpr int kPfMinWG = 2;               // workgroups per CU the kernel is built for
+constexpr int kPfBK = 32;                 // K per stage (32 or 64)
+constexpr int kPfRowB = kPfBK * 2;        // bytes per row per stage
+constexpr int kPfCpr = kPfRowB / 16;      // 16-byte chunks per row
+constexpr int kPfRpi = 1024 / kPfRowB;    // rows per fetch instruction
+constexpr int kPfRpw = 256 / kPfRowB;     // rows per 256-byte bank window
+constexpr int kPfAStage = kPfBM * kPfRowB;
+constexpr int kPfStage = kPfAStage + kPfBN * kPfRowB;
+constexpr int kPfLds = kPfStages * kPfStage;
+constexpr int kPfRB = kPfWR / 32;                        // row blocks per wave
+constexpr int kPfWaves = (kPfBM / kPfWR) * (kPfBN / 64); // each wave: kPfWR x 64
+constexpr int kPfInstr = (kPfBM + kPfBN) / kPfRpi / kPfWaves;  // fetch instructions per wave
+static_assert((kPfBM + kPfBN) / kPfRpi % kPfWaves == 0, "fetch split");
+static_assert(kPfBK == 32 || kPfBK == 64, "K step");
+// Swizzle: chunk c of stage row r sits at position c ^ key(r), key(r) =
+// (r / kPfRpw) % kPfCpr, so the 16 rows one ds_read_b128 pass serves fall in
+// 16 distinct 16-byte bank groups of the 256-byte bank window.
 constexpr unsigned kPfMaxTokens = 262144;
 
 enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
@@ -61,7 +84,7 @@ enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
 // the host's debug path at these fixed offsets.
 struct PfLayout {
   size_t ids, rw, logits, sgw, meta, sorted, after, h2, act, y, total;
-  unsigned ld_logits, max_tiles;
+  unsigned ld_logits, max_tiles, max_rows;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -69,17 +92,18 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 PfLayout pf_layout(unsigned T, unsigned E) {
   PfLayout L;
   L.ld_logits = (E + 1 + 7) & ~7u;
-  L.max_tiles = (9u * T + kPfBM - 1) / kPfBM + E + 1;
+  L.max_tiles = (9u * T + kPfBM - 1) / kPfBM + E + 1;   // sum over groups of ceil(n / 256)
+  L.max_rows = 9u * T + (kPfPad - 1) * (E + 1);         // sum of n rounded up to 32
   size_t o = 0;
   L.ids = o;     o = align256(o + (size_t)T * kMoeTopK * 4);
   L.rw = o;      o = align256(o + (size_t)T * kMoeTopK * 4);
   L.logits = o;  o = align256(o + (size_t)T * L.ld_logits * 2);
   L.sgw = o;     o = align256(o + (size_t)T * 4);
-  L.meta = o;    o = align256(o + (size_t)(L.max_tiles + 1) * 4);
-  L.sorted = o;  o = align256(o + (size_t)L.max_tiles * kPfBM * 4);
+  L.meta = o;    o = align256(o + (size_t)(L.max_tiles + 1) * 16);
+  L.sorted = o;  o = align256(o + (size_t)L.max_rows * 4);
   L.after = o;   o = align256(o + (size_t)T * kMoeHidden * 2);
   L.h2 = o;      o = align256(o + (size_t)T * kMoeHidden * 2);
-  L.act = o;     o = align256(o + (size_t)L.max_tiles * kPfBM * kMoeInter * 2);
+  L.act = o;     o = align256(o + (size_t)L.max_rows * kMoeInter * 2);
   L.y = o;       o = align256(o + (size_t)9 * T * kMoeHidden * 2);
   L.total = o;
   return L;
@@ -147,49 +171,116 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
   if (lane == 0) sgw[t] = bf2f(f2bf(1.0f / (1.0f + expf(-bf2f(row[E])))));
 }
 
-// ---- 4. slots sorted by group, each group padded to 64-row tiles ----------
-// meta[0] = number of tiles, meta[1 + i] = group of tile i; sorted[p] = slot
-// (t * 8 + k for routed rank k of token t, 8T + t for the shared expert) or
-// -1 for padding.  Order inside a group is arbitrary: every row of the GEMMs
-// is computed independently, so it does not affect any value.
+// ---- 4. slots sorted by group, groups padded to 32 rows, 256-row tiles ----
+// sorted[p] = slot (t * 8 + k for routed rank k of token t, 8T + t for the
+// shared expert) or -1 for padding; group g occupies rows [row_off[g],
+// row_off[g] + roundup32(n_g)).  meta (int4) [0] = {tiles}, [1 + i] =
+// {group, first row, rows (1..256), 0} for tile i.  Order inside a group is
+// arbitrary: every row of the GEMMs is computed independently, so it does not
+// affect any value.
 __global__ __launch_bounds__(1024) void moe_align_kernel(
-    const int* __restrict__ ids, unsigned T, unsigned E, int* __restrict__ meta,
+    const int* __restrict__ ids, unsigned T, unsigned E, int4* __restrict__ meta,
     int* __restrict__ sorted) {
   __shared__ int cnt[kMoeMaxExperts + 1];
+  __shared__ int row_off[kMoeMaxExperts + 2];
   __shared__ int tile_off[kMoeMaxExperts + 2];
   __shared__ int wpos[kMoeMaxExperts + 1];
   const unsigned G = E + 1, tid = threadIdx.x, routed = kMoeTopK * T;
+  const int4* ids4 = reinterpret_cast<const int4*>(ids);   // 8T ids: whole int4s
+  const unsigned n4 = routed / 4;
+  constexpr unsigned kBatch = 4;                            // int4 loads in flight per thread
   for (unsigned g = tid; g < G; g += blockDim.x) cnt[g] = 0;
   __syncthreads();
-  for (unsigned i = tid; i < routed; i += blockDim.x) atomicAdd(&cnt[ids[i]], 1);
+  for (unsigned i0 = tid; i0 < n4; i0 += kBatch * blockDim.x) {
+    int4 v[kBatch];
+#pragma unroll
+    for (unsigned u = 0; u < kBatch; ++u) {
+      const unsigned i = i0 + u * blockDim.x;
+      v[u] = i < n4 ? ids4[i] : int4{-1, -1, -1, -1};
+    }
+#pragma unroll
+    for (unsigned u = 0; u < kBatch; ++u) {
+      if (v[u].x >= 0) {
+        atomicAdd(&cnt[v[u].x], 1);
+        atomicAdd(&cnt[v[u].y], 1);
+        atomicAdd(&cnt[v[u].z], 1);
+        atomicAdd(&cnt[v[u].w], 1);
+      }
+    }
+  }
   __syncthreads();
-  if (tid == 0) {
-    cnt[E] = (int)T;
-    tile_off[0] = 0;
-    for (unsigned g = 0; g < G; ++g) tile_off[g + 1] = tile_off[g] + (cnt[g] + kPfBM - 1) / kPfBM;
-    meta[0] = tile_off[G];
+  if (tid < 64) {   // one wave: exclusive scans of padded rows and tiles per group
+    constexpr int kPer = (kMoeMaxExperts + 1 + 63) / 64;   // 5 groups per lane
+    int rows[kPer], tiles[kPer], rsum = 0, tsum = 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const unsigned g = tid * kPer + j;
+      const int c = g < E ? cnt[g] : (g == E ? (int)T : 0);
+      rows[j] = (c + kPfPad - 1) / kPfPad * kPfPad;
+      tiles[j] = (c + kPfBM - 1) / kPfBM;
+      rsum += rows[j];
+      tsum += tiles[j];
+    }
+    int rincl = rsum, tincl = tsum;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int ru = __shfl_up(rincl, o, 64), tu = __shfl_up(tincl, o, 64);
+      if ((int)tid >= o) {
+        rincl += ru;
+        tincl += tu;
+      }
+    }
+    int roff = rincl - rsum, toff = tincl - tsum;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const unsigned g = tid * kPer + j;
+      if (g <= G) {   // [G] = totals
+        row_off[g] = roff;
+        tile_off[g] = toff;
+      }
+      roff += rows[j];
+      toff += tiles[j];
+    }
+    if (tid == 63) meta[0] = int4{tincl, 0, 0, 0};
+    if (tid == 0) cnt[E] = (int)T;
   }
   __syncthreads();
   for (unsigned g = tid; g < G; g += blockDim.x) {
-    wpos[g] = tile_off[g] * kPfBM;
-    for (int i = tile_off[g]; i < tile_off[g + 1]; ++i) meta[1 + i] = (int)g;
-    for (int p = tile_off[g] * kPfBM + cnt[g]; p < tile_off[g + 1] * kPfBM; ++p) sorted[p] = -1;
+    const int c = cnt[g], r0 = row_off[g];
+    wpos[g] = r0;
+    for (int j = 0; j < tile_off[g + 1] - tile_off[g]; ++j)
+      meta[1 + tile_off[g] + j] = int4{(int)g, r0 + kPfBM * j, min(kPfBM, c - kPfBM * j), 0};
+    for (int p = r0 + c; p < row_off[g + 1]; ++p) sorted[p] = -1;
   }
   __syncthreads();
-  for (unsigned i = tid; i < routed; i += blockDim.x) {
-    const int p = atomicAdd(&wpos[ids[i]], 1);
-    sorted[p] = (int)i;
+  for (unsigned i0 = tid; i0 < n4; i0 += kBatch * blockDim.x) {
+    int4 v[kBatch];
+#pragma unroll
+    for (unsigned u = 0; u < kBatch; ++u) {
+      const unsigned i = i0 + u * blockDim.x;
+      v[u] = i < n4 ? ids4[i] : int4{-1, -1, -1, -1};
+    }
+#pragma unroll
+    for (unsigned u = 0; u < kBatch; ++u) {
+      if (v[u].x >= 0) {
+        const int i = 4 * (int)(i0 + u * blockDim.x);
+        sorted[atomicAdd(&wpos[v[u].x], 1)] = i;
+        sorted[atomicAdd(&wpos[v[u].y], 1)] = i + 1;
+        sorted[atomicAdd(&wpos[v[u].z], 1)] = i + 2;
+        sorted[atomicAdd(&wpos[v[u].w], 1)] = i + 3;
+      }
+    }
   }
-  const int shared0 = tile_off[E] * kPfBM;
+  const int shared0 = row_off[E];
   for (unsigned t = tid; t < T; t += blockDim.x) sorted[shared0 + t] = (int)(routed + t);
 }
 
 // ---- 2/5/6. grouped GEMM ----------------------------------------------------
 struct GemmArgs {
-  const bf16* a;            // h2 [T, 2048] (router, gate/up) or act [tiles*64, 512] (down)
+  const bf16* a;            // h2 [T, 2048] (router, gate/up) or act [rows, 512] (down)
   const bf16* w;            // router: w_in; gate/up: expert_gate_up; down: expert_down
   const bf16* w_shared;     // gate/up: shared [gate_proj | up_proj]; down: shared_down
-  const int* meta;
+  const int4* meta;
   const int* sorted;
   const float* rw;
   const float* sgw;
@@ -211,33 +302,89 @@ __device__ __forceinline__ u32x4 buffer_rsrc(const void* base, unsigned bytes) {
 constexpr unsigned kOob = 0x80000000u;   // a row offset past every buffer's range
 
 template <int MODE>
-__global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kPfStage];
-  __shared__ int row_slot[kPfBM];
-  __shared__ float row_w[kPfBM];
+__host__ __device__ constexpr unsigned n_blocks(unsigned E) {
+  return MODE == kRouter ? (E + 1 + kPfBN - 1) / kPfBN
+                         : (MODE == kGateUp ? kMoeInter / (kPfBN / 2) : kMoeHidden / kPfBN);
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations of
+// this wave are outstanding (expcnt and lgkmcnt not waited on).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// The K loop for a wave computing NRB (0..kPfRB) row blocks of 32.  Every
+// wave fetches and meets the barriers whatever its NRB.  Stage s of the ring
+// holds K step s mod kPfStages; the fetch of step + kPfStages - 1 is issued
+// once every wave has finished reading step - 1.
+template <int NRB, int NSTEPS, typename Fetch>
+__device__ __forceinline__ void gemm_k_loop(Fetch& fetch, const char* lds, int arow, int brow0,
+                                            int brow1, const int (&koff)[kPfBK / 16],
+                                            f32x16 (&acc)[kPfRB][2]) {
+#pragma unroll
+  for (int st = 0; st < kPfStages - 1; ++st) fetch(st);
+  for (int step = 0; step < NSTEPS; ++step) {
+    // this wave's fetches of `step` landed (later ones may stay in flight)
+    if (step + kPfStages - 2 < NSTEPS)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((kPfStages - 2) * kPfInstr));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();   // every wave's fetches landed; stage (step - 1) is free
+    if (step + kPfStages - 1 < NSTEPS) fetch(step + kPfStages - 1);
+    if constexpr (NRB > 0) {
+      const char* st = lds + (step % kPfStages) * kPfStage;
+#pragma unroll
+      for (int s = 0; s < kPfBK / 16; ++s) {
+        const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(st + brow0 * kPfRowB + koff[s]);
+        const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(st + brow1 * kPfRowB + koff[s]);
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(
+              st + (arow + 32 * rb) * kPfRowB + koff[s]);
+          acc[rb][0] = mfma32x32x16(a, b0, acc[rb][0]);
+          acc[rb][1] = mfma32x32x16(a, b1, acc[rb][1]);
+        }
+      }
+    }
+  }
+}
+
+// Wave (wm = w % (BM / WR), wn = w / (BM / WR)) computes tile rows
+// WR wm + 32 rb against weight rows (gate/up: gate 32wn.. and up BN/2 +
+// 32wn.., i.e. act columns 32wn..; else 64wn.. and 64wn + 32..).  Fetch
+// instruction i (of (BM + BN) / 8) moves rows 8i..8i+7 of the stage: A rows
+// first, then B rows; wave w issues instructions w * kPfInstr + j.
+template <int MODE>
+__global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmArgs p) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int K = MODE == kDown ? kMoeInter : kMoeHidden;
   constexpr int nsteps = K / kPfBK;
-  const unsigned n_tiles_n = MODE == kRouter ? (p.E + 1 + kPfBN - 1) / kPfBN
-                                             : (MODE == kGateUp ? kMoeInter / 64 : kMoeHidden / kPfBN);
-  const unsigned m_tiles = MODE == kRouter ? (p.T + kPfBM - 1) / kPfBM : (unsigned)p.meta[0];
-  const unsigned items = m_tiles * n_tiles_n;
+  const unsigned nb = n_blocks<MODE>(p.E);
+  const unsigned m_tiles = MODE == kRouter ? (p.T + kPfBM - 1) / kPfBM : (unsigned)p.meta[0].x;
+  const unsigned items = m_tiles * nb;
   const unsigned share = (items + 7) / 8;
   const unsigned xi = blockIdx.x >> 3;
   if (xi >= share) return;
   const unsigned item = (blockIdx.x & 7) * share + xi;
   if (item >= items) return;
-  const unsigned mt = item / n_tiles_n, nt = item % n_tiles_n;
-  const int group = MODE == kRouter ? 0 : p.meta[1 + mt];
+  const unsigned mt = item / nb, nt = item % nb;
+  int group = 0, row0, rows;
+  if constexpr (MODE == kRouter) {
+    row0 = (int)(mt * kPfBM);
+    rows = min(kPfBM, (int)p.T - row0);
+  } else {
+    const int4 m = p.meta[1 + mt];
+    group = m.x;
+    row0 = m.y;
+    rows = m.z;
+  }
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
 
   // Operand sources (buffer resources: out-of-range rows read as zero).
   u32x4 ars, brs;
-  if constexpr (MODE == kDown) {
-    ars = buffer_rsrc(p.a + (size_t)mt * kPfBM * kMoeInter, kPfBM * kMoeInter * 2);
-  } else {
+  if constexpr (MODE == kDown)
+    ars = buffer_rsrc(p.a + (size_t)row0 * kMoeInter, (unsigned)rows * kMoeInter * 2u);
+  else
     ars = buffer_rsrc(p.a, p.T * (unsigned)kMoeHidden * 2u);
-  }
   if constexpr (MODE == kRouter) {
     brs = buffer_rsrc(p.w, (p.E + 1) * (unsigned)kMoeHidden * 2u);
   } else if constexpr (MODE == kGateUp) {
@@ -250,122 +397,120 @@ __global__ __launch_bounds__(256, 2) void moe_gemm_kernel(GemmArgs p) {
     brs = buffer_rsrc(wg, (unsigned)kMoeHidden * kMoeInter * 2u);
   }
 
-  // Per-lane fetch offsets: wave w fills A instructions 2w, 2w+1 (8 rows each)
-  // and B instructions 4w..4w+3; lane = (row in the 8, chunk position), and
-  // the source chunk is position ^ row so LDS holds the swizzled layout.
-  const int r8 = lane >> 3, cpos = lane & 7;
-  const int csrc = (cpos ^ r8) * 16;
-  unsigned a_off[2], b_off[4];
+  // Fetch plan: one instruction moves 8 rows of 128 bytes (lane = row in the
+  // 8 x chunk position; the source chunk is position ^ row, so LDS holds the
+  // swizzled layout).  A instructions whose rows are all past the tile's rows
+  // are skipped.
+  const int rin = lane / kPfCpr, cpos = lane % kPfCpr;   // row in the instruction, chunk
+  unsigned f_off[kPfInstr];
+  u32x4 f_rs[kPfInstr];
+  bool f_live[kPfInstr];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = (2 * wave + j) * 8 + r8;   // tile row 0..63
+  for (int j = 0; j < kPfInstr; ++j) {
+    const int ins = wave * kPfInstr + j;
+    const bool is_a = ins < kPfBM / kPfRpi;
     unsigned off;
-    if constexpr (MODE == kRouter) {
-      const unsigned t = mt * kPfBM + r;
-      off = t < p.T ? t * (unsigned)kMoeHidden * 2u : kOob;
-    } else if constexpr (MODE == kGateUp) {
-      const int slot = p.sorted[mt * kPfBM + r];
-      const unsigned routed = kMoeTopK * p.T;
-      const unsigned t = slot < 0 ? 0u : ((unsigned)slot < routed ? (unsigned)slot / kMoeTopK
-                                                                  : (unsigned)slot - routed);
-      off = slot < 0 ? kOob : t * (unsigned)kMoeHidden * 2u;
+    if (is_a) {
+      const int r = ins * kPfRpi + rin;
+      if constexpr (MODE == kRouter) {
+        off = r < rows ? (unsigned)(row0 + r) * kMoeHidden * 2u : kOob;
+      } else if constexpr (MODE == kGateUp) {
+        const int slot = r < rows ? p.sorted[row0 + r] : -1;
+        const unsigned routed = kMoeTopK * p.T;
+        const unsigned t = slot < 0 ? 0u : ((unsigned)slot < routed ? (unsigned)slot / kMoeTopK
+                                                                    : (unsigned)slot - routed);
+        off = slot < 0 ? kOob : t * (unsigned)kMoeHidden * 2u;
+      } else {
+        off = (unsigned)r * kMoeInter * 2u;
+      }
     } else {
-      off = (unsigned)r * kMoeInter * 2u;
+      const int r = (ins - kPfBM / kPfRpi) * kPfRpi + rin;
+      unsigned row;
+      if constexpr (MODE == kGateUp)
+        row = r < kPfBN / 2 ? nt * (kPfBN / 2) + r : kMoeInter + nt * (kPfBN / 2) + (r - kPfBN / 2);
+      else
+        row = nt * kPfBN + r;
+      off = row * (unsigned)K * 2u;
     }
-    a_off[j] = off + csrc;
-  }
+    const int srow = ins * kPfRpi + rin;   // stage row this lane fills
+    f_off[j] = off + ((cpos ^ ((srow / kPfRpw) % kPfCpr)) * 16);
+    f_live[j] = !is_a || ins * kPfRpi < rows;
+    const u32x4 r = is_a ? ars : brs;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = (4 * wave + j) * 8 + r8;   // tile weight row 0..127
-    unsigned row;
-    if constexpr (MODE == kGateUp)
-      row = r < 64 ? nt * 64 + r : kMoeInter + nt * 64 + (r - 64);
-    else
-      row = nt * kPfBN + r;
-    b_off[j] = row * (unsigned)K * 2u + csrc;
+    for (int c = 0; c < 4; ++c) f_rs[j][c] = __builtin_amdgcn_readfirstlane(r[c]);
   }
-  if constexpr (MODE == kDown) {
-    if (tid < kPfBM) {
-      const int slot = p.sorted[mt * kPfBM + tid];
-      const unsigned routed = kMoeTopK * p.T;
-      row_slot[tid] = slot;
-      row_w[tid] = slot < 0 ? 0.f : ((unsigned)slot < routed ? p.rw[slot] : p.sgw[slot - routed]);
-    }
-  }
-
   const unsigned lds0 = static_cast<unsigned>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds));
-  auto fetch = [&](int step, int stage) {
-    const unsigned sbase = lds0 + stage * kPfStage;
+  auto fetch = [&](int step) {
+    const unsigned sbase = lds0 + (step % kPfStages) * kPfStage;
     const unsigned kb = (unsigned)step * kPfRowB;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      fetch_rows(sbase + ((2 * wave + j) * 8) * kPfRowB, (int)(a_off[j] + kb), ars);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      fetch_rows(sbase + kPfAStage + ((4 * wave + j) * 8) * kPfRowB, (int)(b_off[j] + kb), brs);
+    for (int j = 0; j < kPfInstr; ++j) {
+      // a skipped instruction is replaced by a dummy in-range load so that
+      // every wave keeps the same count of outstanding loads per stage
+      const int ins = wave * kPfInstr + j;
+      fetch_rows(sbase + ins * kPfRpi * kPfRowB, f_live[j] ? (int)(f_off[j] + kb) : (int)kOob,
+                 f_rs[j]);
+    }
   };
 
-  // MFMA operand addresses: wave (wm, wn) owns rows 32wm.. and weight rows
-  // (gate/up: 32wn.. and 64 + 32wn..; else 64wn.. and 64wn + 32..).
-  const int wm = wave & 1, wn = wave >> 1;
+  constexpr int kWm = kPfBM / kPfWR;
+  const int wm = wave % kWm, wn = wave / kWm;
   const int li = lane & 31, kh = lane >> 5;
-  const int arow = 32 * wm + li;
-  const int brow0 = MODE == kGateUp ? 32 * wn + li : 64 * wn + li;
-  const int brow1 = MODE == kGateUp ? 64 + 32 * wn + li : 64 * wn + 32 + li;
-  int koff[4];
+  const int arow = kPfWR * wm + li;
+  const int brow0 = kPfBM + (MODE == kGateUp ? 32 * wn + li : 64 * wn + li);
+  const int brow1 = kPfBM + (MODE == kGateUp ? kPfBN / 2 + 32 * wn + li : 64 * wn + 32 + li);
+  int koff[kPfBK / 16];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) koff[s] = (((2 * s + kh) ^ (lane & 7)) * 16);
+  for (int s = 0; s < kPfBK / 16; ++s) koff[s] = (((2 * s + kh) ^ ((li / kPfRpw) % kPfCpr)) * 16);
+  const int nrb = min(kPfRB, max(0, (rows - kPfWR * wm + 31) / 32));
 
-  f32x16 acc0 = f32x16{}, acc1 = f32x16{};
-  fetch(0, 0);
-  for (int step = 0; step < nsteps; ++step) {
-    const int stage = step & 1;
-    __builtin_amdgcn_s_waitcnt(0);   // this wave's fetches of this step landed
-    __syncthreads();                 // ... and every wave's; the other stage is free
-    if (step + 1 < nsteps) fetch(step + 1, stage ^ 1);
-    const char* sa = lds + stage * kPfStage;
-    const char* sb = sa + kPfAStage;
+  f32x16 acc[kPfRB][2];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const bf16x8 af = *reinterpret_cast<const bf16x8*>(sa + arow * kPfRowB + koff[s]);
-      const bf16x8 b0 = *reinterpret_cast<const bf16x8*>(sb + brow0 * kPfRowB + koff[s]);
-      const bf16x8 b1 = *reinterpret_cast<const bf16x8*>(sb + brow1 * kPfRowB + koff[s]);
-      acc0 = mfma32x32x16(af, b0, acc0);
-      acc1 = mfma32x32x16(af, b1, acc1);
+  for (int i = 0; i < kPfRB; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+  if (nrb == 0) {
+    gemm_k_loop<0, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc);
+  } else if constexpr (kPfRB == 1) {
+    gemm_k_loop<1, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc);
+  } else if constexpr (kPfRB == 2) {
+    if (nrb == 1) gemm_k_loop<1, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc);
+    else gemm_k_loop<2, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc);
+  } else {
+    switch (nrb) {
+      case 1: gemm_k_loop<1, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc); break;
+      case 2: gemm_k_loop<2, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc); break;
+      case 3: gemm_k_loop<3, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc); break;
+      default: gemm_k_loop<kPfRB, nsteps>(fetch, lds, arow, brow0, brow1, koff, acc); break;
     }
   }
 
-  // Lane holds rows 32wm + 8(i/4) + 4kh + i%4 of weight rows brow0 / brow1.
-  if constexpr (MODE == kRouter) {
-    const unsigned n0 = nt * kPfBN + 64 * wn + li, n1 = n0 + 32;
+  // acc[rb][cb][i] = tile row WR wm + 32rb + 8(i/4) + 4kh + i%4, weight row
+  // brow_cb.
+  const unsigned routed = kMoeTopK * p.T;
+#pragma unroll
+  for (int rb = 0; rb < kPfRB; ++rb) {
+    if (rb >= nrb) break;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const unsigned t = mt * kPfBM + 32 * wm + 8 * (i >> 2) + 4 * kh + (i & 3);
-      if (t < p.T) {
-        if (n0 <= p.E) p.out[(size_t)t * p.ld_out + n0] = f2bf(acc0[i]);
-        if (n1 <= p.E) p.out[(size_t)t * p.ld_out + n1] = f2bf(acc1[i]);
-      }
-    }
-  } else if constexpr (MODE == kGateUp) {
-    const unsigned c = nt * 64 + 32 * wn + li;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const unsigned r = mt * kPfBM + 32 * wm + 8 * (i >> 2) + 4 * kh + (i & 3);
-      const float g = bf2f(f2bf(acc0[i])), u = bf2f(f2bf(acc1[i]));
-      p.out[(size_t)r * kMoeInter + c] = f2bf(silu_f(g) * u);
-    }
-  } else {
-    const unsigned n0 = nt * kPfBN + 64 * wn + li, n1 = n0 + 32;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int r = 32 * wm + 8 * (i >> 2) + 4 * kh + (i & 3);
-      const int slot = row_slot[r];
-      if (slot >= 0) {
-        const float w = row_w[r];
-        bf16* y = p.out + (size_t)slot * kMoeHidden;
-        y[n0] = f2bf(bf2f(f2bf(acc0[i])) * w);
-        y[n1] = f2bf(bf2f(f2bf(acc1[i])) * w);
+      const int r = kPfWR * wm + 32 * rb + 8 * (i >> 2) + 4 * kh + (i & 3);
+      if (r >= rows) continue;
+      if constexpr (MODE == kRouter) {
+        const unsigned n = nt * kPfBN + 64 * wn + li;
+        bf16* o = p.out + (size_t)(row0 + r) * p.ld_out;
+        if (n <= p.E) o[n] = f2bf(acc[rb][0][i]);
+        if (n + 32 <= p.E) o[n + 32] = f2bf(acc[rb][1][i]);
+      } else if constexpr (MODE == kGateUp) {
+        const unsigned c = nt * (kPfBN / 2) + 32 * wn + li;
+        const float g = bf2f(f2bf(acc[rb][0][i])), u = bf2f(f2bf(acc[rb][1][i]));
+        p.out[(size_t)(row0 + r) * kMoeInter + c] = f2bf(silu_f(g) * u);
+      } else {
+        const int slot = p.sorted[row0 + r];
+        const float w = (unsigned)slot < routed ? p.rw[slot] : p.sgw[slot - routed];
+        bf16* y = p.out + (size_t)slot * kMoeHidden + nt * kPfBN + 64 * wn + li;
+        y[0] = f2bf(bf2f(f2bf(acc[rb][0][i])) * w);
+        y[32] = f2bf(bf2f(f2bf(acc[rb][1][i])) * w);
       }
     }
   }
@@ -439,13 +584,23 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
       !aligned16(workspace))
     return Q36_EINVAL;
   const unsigned T = tokens, E = n_experts;
+  static bool attr_set = false;   // 80 KiB of dynamic LDS per GEMM workgroup
+  if (!attr_set) {
+    for (const void* f : {reinterpret_cast<const void*>(moe_gemm_kernel<kRouter>),
+                          reinterpret_cast<const void*>(moe_gemm_kernel<kGateUp>),
+                          reinterpret_cast<const void*>(moe_gemm_kernel<kDown>)}) {
+      const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds);
+      if (e != hipSuccess) return (int)e;
+    }
+    attr_set = true;
+  }
   const PfLayout L = pf_layout(T, E);
   char* ws = static_cast<char*>(workspace);
   int* ids = reinterpret_cast<int*>(ws + L.ids);
   float* rw = reinterpret_cast<float*>(ws + L.rw);
   bf16* logits = reinterpret_cast<bf16*>(ws + L.logits);
   float* sgw = reinterpret_cast<float*>(ws + L.sgw);
-  int* meta = reinterpret_cast<int*>(ws + L.meta);
+  int4* meta = reinterpret_cast<int4*>(ws + L.meta);
   int* sorted = reinterpret_cast<int*>(ws + L.sorted);
   bf16* after = reinterpret_cast<bf16*>(ws + L.after);
   bf16* h2 = reinterpret_cast<bf16*>(ws + L.h2);
@@ -472,9 +627,9 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   g.w = win;
   g.out = logits;
   g.ld_out = L.ld_logits;
-  const unsigned router_items = ((T + kPfBM - 1) / kPfBM) * ((E + 1 + kPfBN - 1) / kPfBN);
+  const unsigned router_items = ((T + kPfBM - 1) / kPfBM) * n_blocks<kRouter>(E);
   g.max_items = router_items;
-  hipLaunchKernelGGL(moe_gemm_kernel<kRouter>, grid_for(router_items), dim3(256), 0, st, g);
+  hipLaunchKernelGGL(moe_gemm_kernel<kRouter>, grid_for(router_items), dim3(64 * kPfWaves), kPfLds, st, g);
 
   hipLaunchKernelGGL(moe_topk_kernel, dim3(tok_blocks), dim3(256), 0, st, logits,
                      L.ld_logits, E, T, ids, rw, sgw);
@@ -484,15 +639,15 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   g.w = static_cast<const bf16*>(expert_gate_up);
   g.w_shared = win + (size_t)(E + 1) * kMoeHidden;
   g.out = act;
-  g.max_items = L.max_tiles * (kMoeInter / 64);
-  hipLaunchKernelGGL(moe_gemm_kernel<kGateUp>, grid_for(g.max_items), dim3(256), 0, st, g);
+  g.max_items = L.max_tiles * n_blocks<kGateUp>(E);
+  hipLaunchKernelGGL(moe_gemm_kernel<kGateUp>, grid_for(g.max_items), dim3(64 * kPfWaves), kPfLds, st, g);
 
   g.a = act;
   g.w = static_cast<const bf16*>(expert_down);
   g.w_shared = static_cast<const bf16*>(shared_down);
   g.out = y;
-  g.max_items = L.max_tiles * (kMoeHidden / kPfBN);
-  hipLaunchKernelGGL(moe_gemm_kernel<kDown>, grid_for(g.max_items), dim3(256), 0, st, g);
+  g.max_items = L.max_tiles * n_blocks<kDown>(E);
+  hipLaunchKernelGGL(moe_gemm_kernel<kDown>, grid_for(g.max_items), dim3(64 * kPfWaves), kPfLds, st, g);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, st, y, after,
                      static_cast<bf16*>(out), T);

@@ -44,7 +44,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
-    p.add_argument("--only", choices=["decode", "prefill", "gdn", "copy"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "gdn", "moe", "copy"], default=None,
                    help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
 
@@ -335,6 +335,65 @@ def bench_moe_decode(torch, dev, layers, iters, warmup, use_graph, seed=7):
             "hbm_gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def moe_prefill_flops(tokens, n_experts=256):
+    """Algorithmic FLOP of one MoE block over `tokens` tokens: router +
+    shared-gate GEMM (E + 1 rows) and, for 8 routed rows plus the shared
+    expert per token, gate/up (2 x 2048 x 1024) and down (2 x 512 x 2048)."""
+    return tokens * (2 * 2048 * (n_experts + 1) + 9 * (2 * 2048 * 1024 + 2 * 512 * 2048))
+
+
+def bench_moe_prefill(torch, dev, tokens, iters, warmup, native=True, seed=11):
+    """One MoE block over `tokens` prefill tokens (256 experts, top-8).  The
+    torch leg runs the same routed rows as a loop of per-expert hipBLASLt
+    GEMMs (torch.matmul) after the native kernel's routing, which it does not
+    time."""
+    from qwen36_attn.moe import MoEBlock
+    import torch.nn.functional as F
+    gen = torch.Generator(device=dev).manual_seed(seed)
+
+    def rnd(shape, std):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(torch.bfloat16)
+    w = {"post_attention_layernorm": rnd((2048,), 0.1), "router": rnd((256, 2048), 0.05),
+         "expert_gate_up": rnd((256, 1024, 2048), 0.02), "expert_down": rnd((256, 2048, 512), 0.02),
+         "shared_gate": rnd((1, 2048), 0.02), "shared_gate_proj": rnd((512, 2048), 0.02),
+         "shared_up_proj": rnd((512, 2048), 0.02), "shared_down_proj": rnd((2048, 512), 0.02)}
+    block = MoEBlock(w)
+    x = rnd((tokens, 2048), 0.5)
+    a = rnd((tokens, 2048), 0.5)
+    out = torch.empty(tokens, 2048, dtype=torch.bfloat16, device=dev)
+    if native:
+        fn = lambda: block.prefill(x, a, out=out)  # noqa: E731
+    else:
+        _, ids, rw, _, _ = block.prefill(x, a, debug=True)
+        flat = ids.view(-1).long()
+        groups = [(e, (flat == e).nonzero().squeeze(1)) for e in range(256)]
+        groups = [(e, r) for e, r in groups if r.numel()]
+        rwb = rw.view(-1, 1).to(torch.bfloat16)
+        y = torch.empty(tokens * 8, 2048, dtype=torch.bfloat16, device=dev)
+
+        def fn():
+            after = x + a
+            h2 = (after.float() * torch.rsqrt(after.float().pow(2).mean(-1, keepdim=True) + 1e-6)
+                  * (w["post_attention_layernorm"].float() + 1)).to(torch.bfloat16)
+            h2 @ block.w_in[:257].t()
+            for e, rows in groups:
+                gu = h2[rows // 8] @ w["expert_gate_up"][e].t()
+                act = (F.silu(gu[:, :512].float()) * gu[:, 512:].float()).to(torch.bfloat16)
+                y[rows] = act @ w["expert_down"][e].t()
+            moe = (y * rwb).view(tokens, 8, 2048).sum(1)
+            su = h2 @ block.w_in[257:].t()
+            sact = (F.silu(su[:, :512].float()) * su[:, 512:].float()).to(torch.bfloat16)
+            out.copy_(after + (moe + sact @ w["shared_down_proj"].t()))
+    ms = Timer(torch).time(fn, iters, warmup)
+    flops = moe_prefill_flops(tokens)
+    wbytes = 256 * (1024 * 2048 + 2048 * 512) * 2
+    del block, w
+    torch.cuda.empty_cache()
+    return {"tokens": tokens, "ms": ms, "tflops": flops / (ms * 1e-3) / 1e12,
+            "frac_mfma": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "expert_weight_bytes": wbytes}
+
+
 def causal_pairs(t, s):
     off = s - t
     return t * off + t * (t + 1) // 2
@@ -484,6 +543,9 @@ def run_only(torch, fa, dev, args):
         r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
+    elif args.only == "moe":
+        r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup),
+             bench_moe_prefill(torch, dev, 1024, args.steps, args.warmup)]
     else:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev)
         x.fill_(1.0)
@@ -534,6 +596,9 @@ def main():
         "gdn_decode_unfused_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5,
                                                              use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
+        "moe_prefill_8k": bench_moe_prefill(torch, dev, 8192, 10, 2),
+        "moe_prefill_1k": bench_moe_prefill(torch, dev, 1024, 20, 3),
+        "moe_prefill_8k_torch_expert_loop": bench_moe_prefill(torch, dev, 8192, 3, 1, native=False),
     }
     extra["attention_us_per_token_128k"] = (head["us_per_token"]
                                             + extra["gdn_recurrent_30layers"]["us_per_token"])
