@@ -544,8 +544,7 @@ def run_only(torch, fa, dev, args):
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
     elif args.only == "moe":
-        r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup),
-             bench_moe_prefill(torch, dev, 1024, args.steps, args.warmup)]
+        r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup)]
     else:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev)
         x.fill_(1.0)
