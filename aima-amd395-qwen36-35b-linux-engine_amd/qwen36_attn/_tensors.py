@@ -31,10 +31,11 @@ _SCRATCH: dict[tuple[str, int], torch.Tensor] = {}
 
 
 def scratch(tag: str, nbytes: int, device: torch.device) -> torch.Tensor:
-    """A reusable, zero-initialised uint8 device buffer of at least ``nbytes``
-    bytes.  Calls that share a tag on one device share the buffer, so they are
-    ordered by the stream they run on (the decode kernel's merge counters rely
-    on the zero fill and leave the buffer zeroed after every call)."""
+    """A reusable uint8 device buffer of at least ``nbytes`` bytes (zeroed
+    when first allocated; the kernels write every workspace byte they read, so
+    no call depends on what an earlier call left there).  Calls that share a
+    tag on one device share the buffer, so they are ordered by the stream they
+    run on."""
     key = (tag, device.index if device.index is not None else torch.cuda.current_device())
     buf = _SCRATCH.get(key)
     if buf is None or buf.numel() < nbytes:
