@@ -135,3 +135,37 @@ def test_conv1d_gating_norm(gpu):
     out = G.gated_rmsnorm(core.to(gpu), z.to(gpu), wn.to(gpu))
     ref = O.gated_rmsnorm(core, z, wn)
     assert (out.cpu().float() - ref.float()).abs().max().item() <= TOL_OUT
+
+
+def test_chunk_prefill_max_tokens_tail(gpu):
+    """T = 262144, the largest accepted: every output finite, and the
+    full-length prefill's last 64 outputs and final state equal the oracle's
+    recurrence over those 64 tokens started from the state the kernels reach
+    after the first T - 64 tokens (a prefill of that prefix: the same chunk
+    sequence)."""
+    from qwen36_attn import gated_deltanet as G
+    t, tail = 262144, 64
+    g = torch.Generator(device=gpu).manual_seed(9)
+    q = torch.randn(t, 16, 128, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(t, 16, 128, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(t, 32, 128, generator=g, device=gpu).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(t, 32, generator=g, device=gpu))
+    a = torch.rand(32, generator=g, device=gpu) * 16.0
+    gg = (-torch.nn.functional.softplus(torch.randn(t, 32, generator=g, device=gpu)) * a).float()
+    print("gdn chunk max tokens", flush=True)
+    out, st = G.chunk_gated_delta_rule(q, k, v, gg, beta, None)
+    out, st = out.clone(), st.clone()
+    _, st_head = G.chunk_gated_delta_rule(q[:-tail], k[:-tail], v[:-tail], gg[:-tail],
+                                          beta[:-tail], None)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item()
+    R = O.repeat_kv_heads
+    ref_o, ref_s = O.recurrent_gated_delta_rule(
+        R(q[-tail:].cpu()).unsqueeze(0), R(k[-tail:].cpu()).unsqueeze(0),
+        v[-tail:].cpu().unsqueeze(0), gg[-tail:].cpu().unsqueeze(0),
+        beta[-tail:].cpu().float().unsqueeze(0), st_head.cpu().reshape(1, 32, 128, 128))
+    got = out.reshape(t, -1)[-tail:].cpu().float()
+    assert (got - ref_o.float().reshape(tail, -1)).abs().max().item() <= TOL_OUT
+    assert rel_err(st.cpu(), ref_s.reshape(st.shape)) <= TOL_STATE
+    del q, k, v, beta, gg, out
+    torch.cuda.empty_cache()

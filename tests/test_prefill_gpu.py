@@ -128,3 +128,28 @@ def test_prefill_overflowing_jump_rescale(gpu):
     ref = O.prefill_attention(q, k, v, position_start=0, out_dtype=torch.float32)
     assert torch.isfinite(got).all()
     assert (got - ref).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("t,s", [(262144, 262144), (131072, 262144)])
+def test_prefill_max_tokens_sampled_rows(gpu, t, s):
+    """The largest sizes the provider accepts (262144 tokens; square and
+    bottom-right): inputs drawn on the device, every output finite, and rows
+    spread over the range (first, tile edges, last) against the oracle
+    restricted to those rows."""
+    from qwen36_attn.full_attention import fmha_prefill
+    g = torch.Generator(device=gpu).manual_seed(262 + t)
+    q = torch.randn(t, 16, 256, generator=g, device=gpu).to(torch.bfloat16)
+    k = torch.randn(s, 2, 256, generator=g, device=gpu).to(torch.bfloat16)
+    v = torch.randn(s, 2, 256, generator=g, device=gpu).to(torch.bfloat16)
+    print(f"prefill max T={t} S={s}", flush=True)
+    got = fmha_prefill(q, k, v)
+    assert torch.isfinite(got).all().item()
+    kc, vc = k.cpu(), v.cpu()
+    off = s - t
+    for r in [0, 255, 256, t // 2 + 37, t - 257, t - 1]:
+        lim = r + off + 1
+        ref = O.prefill_attention(q[r:r + 1].cpu(), kc[:lim], vc[:lim], position_start=lim - 1,
+                                  out_dtype=torch.float32)
+        assert (got[r:r + 1].cpu() - ref).abs().max().item() <= TOL_TIGHT, r
+    del q, k, v, got
+    torch.cuda.empty_cache()
