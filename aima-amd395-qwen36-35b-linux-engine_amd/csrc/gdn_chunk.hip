@@ -39,6 +39,9 @@
 //    chunk only the state tiles and v' (hi/lo bf16) pass through LDS.
 #include "common.h"
 
+#include <algorithm>
+#include <mutex>
+
 namespace q36 {
 namespace {
 
@@ -158,10 +161,10 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
     unsigned v_token_stride, const float* __restrict__ g,
-    const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws) {
+    const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws, unsigned c0) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PrepLds& s = *reinterpret_cast<PrepLds*>(smem);
-  const unsigned c = blockIdx.x;
+  const unsigned c = c0 + blockIdx.x;
   const int h = blockIdx.y;
   const int kh = h * (int)qk_heads / kGdnHv;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -455,7 +458,7 @@ __device__ __forceinline__ void join_pair(const bf16x8& a, const bf16x8& b,
 // memory in their stored (pre-permuted) order, one chunk ahead.
 __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
     const char* __restrict__ ws, const float* state_in, float* state_out,
-    bf16* __restrict__ out, unsigned tokens, unsigned n_chunks) {
+    bf16* __restrict__ out, unsigned tokens, unsigned c_begin, unsigned c_end) {
   __shared__ ScanLds s;
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int h = 4 * xcd + (slot >> 3);
@@ -570,12 +573,12 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
   // are in flight while chunk c is computed.  Fetches past the last chunk
   // re-read it, keeping every fetch unconditional.
   Stage s0, s1;
-  const unsigned last = n_chunks - 1;
-  fetch(0, s0);
-  for (unsigned c = 0; c < n_chunks; c += 2) {
+  const unsigned last = c_end - 1;
+  fetch(c_begin, s0);
+  for (unsigned c = c_begin; c < c_end; c += 2) {
     fetch(c + 1 < last ? c + 1 : last, s1);
     step(s0, c);
-    if (c + 1 >= n_chunks) break;
+    if (c + 1 >= c_end) break;
     fetch(c + 2 < last ? c + 2 : last, s0);
     step(s1, c + 1);
   }
@@ -584,6 +587,33 @@ __global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
+}
+
+// Prep / scan overlap: a second stream and events per device, created on
+// first use and kept for the life of the process.
+constexpr unsigned kMaxRanges = 8;        // chunk ranges per call
+constexpr unsigned kMinRangeChunks = 16;  // below 2 x 16 chunks: one prep + one scan
+struct Overlap {
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr;
+  hipEvent_t done[kMaxRanges] = {};
+};
+std::mutex g_overlap_mutex;     // one enqueue sequence at a time (shared events)
+Overlap g_overlap[64];
+bool g_overlap_ready[64] = {};
+
+Overlap* overlap_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  Overlap& o = g_overlap[dev];
+  if (!g_overlap_ready[dev]) {
+    if (hipStreamCreateWithFlags(&o.side, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&o.fork, hipEventDisableTiming) != hipSuccess) return nullptr;
+    for (auto& ev : o.done)
+      if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return nullptr;
+    g_overlap_ready[dev] = true;
+  }
+  return &o;
 }
 
 }  // namespace
@@ -621,16 +651,49 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
     attr_set = true;
   }
   char* wsb = static_cast<char*>(workspace);
-  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256),
-                     sizeof(PrepLds), st, static_cast<const bf16*>(q),
-                     static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                     qk_heads, qk_token_stride, v_token_stride,
-                     static_cast<const float*>(g),
-                     static_cast<const float*>(beta), tokens, wsb);
-  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups),
-                     dim3(256), 0, st, wsb,
-                     static_cast<const float*>(state_in),
-                     static_cast<float*>(state_out), static_cast<bf16*>(out),
-                     tokens, n_chunks);
+  const bf16* qb = static_cast<const bf16*>(q);
+  const bf16* kb = static_cast<const bf16*>(k);
+  const bf16* vb = static_cast<const bf16*>(v);
+  const float* gb = static_cast<const float*>(g);
+  const float* bb = static_cast<const float*>(beta);
+  float* so = static_cast<float*>(state_out);
+  auto prep = [&](unsigned c0, unsigned c1, hipStream_t s) {
+    hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(c1 - c0, kGdnHv), dim3(256),
+                       sizeof(PrepLds), s, qb, kb, vb, qk_heads, qk_token_stride,
+                       v_token_stride, gb, bb, tokens, wsb, c0);
+  };
+  auto scan = [&](unsigned c0, unsigned c1, const float* sin) {
+    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(256), 0, st,
+                       wsb, sin, so, static_cast<bf16*>(out), tokens, c0, c1);
+  };
+  const unsigned ranges = std::min(kMaxRanges, n_chunks / kMinRangeChunks);
+  if (ranges < 2) {
+    prep(0, n_chunks, st);
+    scan(0, n_chunks, static_cast<const float*>(state_in));
+    return static_cast<int>(hipGetLastError());
+  }
+  // Prep of chunk range r + 1 overlaps the scan of range r: prep ranges run
+  // in order on a second stream, each scan range waits for its prep range's
+  // event; the state is carried through state_out.
+  std::lock_guard<std::mutex> lock(g_overlap_mutex);
+  Overlap* ov = overlap_for_current_device();
+  if (ov == nullptr) return Q36_EINVAL;
+  hipError_t e = hipEventRecord(ov->fork, st);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ov->side, ov->fork, 0);
+  if (e != hipSuccess) return (int)e;
+  for (unsigned r = 0; r < ranges; ++r) {
+    const unsigned c0 = (unsigned)((uint64_t)n_chunks * r / ranges);
+    const unsigned c1 = (unsigned)((uint64_t)n_chunks * (r + 1) / ranges);
+    prep(c0, c1, ov->side);
+    e = hipEventRecord(ov->done[r], ov->side);
+    if (e != hipSuccess) return (int)e;
+  }
+  for (unsigned r = 0; r < ranges; ++r) {
+    const unsigned c0 = (unsigned)((uint64_t)n_chunks * r / ranges);
+    const unsigned c1 = (unsigned)((uint64_t)n_chunks * (r + 1) / ranges);
+    e = hipStreamWaitEvent(st, ov->done[r], 0);
+    if (e != hipSuccess) return (int)e;
+    scan(c0, c1, r == 0 ? static_cast<const float*>(state_in) : so);
+  }
   return static_cast<int>(hipGetLastError());
 }
