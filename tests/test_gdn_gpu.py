@@ -169,3 +169,40 @@ def test_chunk_prefill_max_tokens_tail(gpu):
     assert rel_err(st.cpu(), ref_s.reshape(st.shape)) <= TOL_STATE
     del q, k, v, beta, gg, out
     torch.cuda.empty_cache()
+
+
+def test_chunk_prefill_graph_replays_match_eager(gpu):
+    """4096 tokens (64 chunks: the prep / scan overlap path with its second
+    stream and events) captured in a graph: three replays, with eager work
+    and synchronisation between them, each bit-identical to the eager call."""
+    from qwen36_attn import gated_deltanet as G
+    t = 4096
+    g = syn.gen(41)
+    q, k, v, gg, beta = syn.gdn_core_inputs(t, g, a_max=1.0)
+    s0 = torch.randn(32, 128, 128, generator=g)
+    qd, kd, vd, gd, bd, sd = _to(gpu, q, k, v, gg, beta, s0)
+    print("gdn chunk graph", flush=True)
+    ref_o, ref_s = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+    ref_o, ref_s = ref_o.clone(), ref_s.clone()
+    out = torch.empty_like(ref_o)
+    fin = torch.empty_like(ref_s)
+
+    def run():
+        o, s = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+        out.copy_(o)
+        fin.copy_(s)
+    run()   # workspace allocated outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run()
+    for i in range(3):
+        out.zero_()
+        fin.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_o), i
+        assert torch.equal(fin, ref_s), i
+        G.chunk_gated_delta_rule(qd[:100], kd[:100], vd[:100], gd[:100], bd[:100], None)
+        torch.cuda.synchronize()
