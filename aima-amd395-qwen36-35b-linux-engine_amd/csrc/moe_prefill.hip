@@ -22,9 +22,10 @@
 //  1. moe_pre_kernel       residual + RMSNorm, one wave per token.
 //  2. moe_gemm<kRouter>    logits [T, E + 1] = h2 [router | shared_gate]^T.
 //  3. moe_topk_kernel      top-8 + routing softmax + shared gate, a wave per token.
-//  4. moe_align_kernel     (token, rank) slots sorted by expert, each group
-//                          padded to 32 rows and cut into tiles of up to 256
-//                          rows; one workgroup.
+//  4. moe_hist/scan/scatter (token, rank) slots sorted by expert, each group
+//                          padded to 32 rows and cut into tiles of up to 128
+//                          rows: per-chunk histograms, one scan workgroup,
+//                          per-chunk scatter.
 //  5. moe_gemm<kGateUp>    act [tile rows, 512] = silu(gate) * up per tile,
 //                          gate and up columns of one group in one workgroup.
 //  6. moe_gemm<kDown>      y rows scaled by their routing weight, scattered to
@@ -49,6 +50,8 @@
 // fetched byte for this tile; the tile shape was chosen from a sweep of
 // 64..256-row x 128..256-column tiles, K steps of 32/64 and 2..4 stages.
 #include "moe_common.h"
+
+#include <algorithm>
 
 namespace q36 {
 namespace {
@@ -76,6 +79,8 @@ static_assert(kPfBK == 32 || kPfBK == 64, "K step");
 // (r / kPfRpw) % kPfCpr, so the 16 rows one ds_read_b128 pass serves fall in
 // 16 distinct 16-byte bank groups of the 256-byte bank window.
 constexpr unsigned kPfMaxTokens = 262144;
+constexpr unsigned kAlignChunk = 4096;    // expert ids per histogram / scatter workgroup (least)
+constexpr unsigned kMaxAlignChunks = 256;
 
 enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
 
@@ -83,8 +88,8 @@ enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
 // three regions (expert ids, routing weights, router logits) are read back by
 // the host's debug path at these fixed offsets.
 struct PfLayout {
-  size_t ids, rw, logits, sgw, meta, sorted, after, h2, act, y, total;
-  unsigned ld_logits, max_tiles, max_rows;
+  size_t ids, rw, logits, sgw, meta, sorted, hist, after, h2, act, y, total;
+  unsigned ld_logits, max_tiles, max_rows, n_chunks, chunk_ids;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -92,7 +97,7 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 PfLayout pf_layout(unsigned T, unsigned E) {
   PfLayout L;
   L.ld_logits = (E + 1 + 7) & ~7u;
-  L.max_tiles = (9u * T + kPfBM - 1) / kPfBM + E + 1;   // sum over groups of ceil(n / 256)
+  L.max_tiles = (9u * T + kPfBM - 1) / kPfBM + E + 1;   // sum over groups of ceil(n / 128)
   L.max_rows = 9u * T + (kPfPad - 1) * (E + 1);         // sum of n rounded up to 32
   size_t o = 0;
   L.ids = o;     o = align256(o + (size_t)T * kMoeTopK * 4);
@@ -101,6 +106,10 @@ PfLayout pf_layout(unsigned T, unsigned E) {
   L.sgw = o;     o = align256(o + (size_t)T * 4);
   L.meta = o;    o = align256(o + (size_t)(L.max_tiles + 1) * 16);
   L.sorted = o;  o = align256(o + (size_t)L.max_rows * 4);
+  // at most kMaxAlignChunks chunks, each a multiple of 1024 ids
+  L.n_chunks = std::min(kMaxAlignChunks, (kMoeTopK * T + kAlignChunk - 1) / kAlignChunk);
+  L.chunk_ids = ((kMoeTopK * T + L.n_chunks - 1) / L.n_chunks + 1023) / 1024 * 1024;
+  L.hist = o;    o = align256(o + (size_t)E * L.n_chunks * 4);
   L.after = o;   o = align256(o + (size_t)T * kMoeHidden * 2);
   L.h2 = o;      o = align256(o + (size_t)T * kMoeHidden * 2);
   L.act = o;     o = align256(o + (size_t)L.max_rows * kMoeInter * 2);
@@ -171,35 +180,36 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
   if (lane == 0) sgw[t] = bf2f(f2bf(1.0f / (1.0f + expf(-bf2f(row[E])))));
 }
 
-// ---- 4. slots sorted by group, groups padded to 32 rows, 256-row tiles ----
+// ---- 4. slots sorted by group, groups padded to 32 rows, 128-row tiles ----
 // sorted[p] = slot (t * 8 + k for routed rank k of token t, 8T + t for the
 // shared expert) or -1 for padding; group g occupies rows [row_off[g],
 // row_off[g] + roundup32(n_g)).  meta (int4) [0] = {tiles}, [1 + i] =
-// {group, first row, rows (1..256), 0} for tile i.  Order inside a group is
-// arbitrary: every row of the GEMMs is computed independently, so it does not
-// affect any value.
-__global__ __launch_bounds__(1024) void moe_align_kernel(
-    const int* __restrict__ ids, unsigned T, unsigned E, int4* __restrict__ meta,
-    int* __restrict__ sorted) {
-  __shared__ int cnt[kMoeMaxExperts + 1];
-  __shared__ int row_off[kMoeMaxExperts + 2];
-  __shared__ int tile_off[kMoeMaxExperts + 2];
-  __shared__ int wpos[kMoeMaxExperts + 1];
-  const unsigned G = E + 1, tid = threadIdx.x, routed = kMoeTopK * T;
-  const int4* ids4 = reinterpret_cast<const int4*>(ids);   // 8T ids: whole int4s
-  const unsigned n4 = routed / 4;
-  constexpr unsigned kBatch = 4;                            // int4 loads in flight per thread
-  for (unsigned g = tid; g < G; g += blockDim.x) cnt[g] = 0;
+// {group, first row, rows, 0} for tile i.  The 8T ids are cut into chunks of
+// kAlignChunk: hist[g][chunk] counts, the scan turns them into each chunk's
+// first row per group, the scatter places the chunk's slots.  Order inside a
+// group is arbitrary: every GEMM row is computed independently, so it does
+// not affect any value.
+
+// 4a. per-chunk expert histogram.
+__global__ __launch_bounds__(256) void moe_hist_kernel(const int* __restrict__ ids, unsigned T,
+                                                       unsigned E, unsigned n_chunks,
+                                                       unsigned chunk_ids,
+                                                       int* __restrict__ hist) {
+  __shared__ int cnt[kMoeMaxExperts];
+  const unsigned tid = threadIdx.x, routed4 = kMoeTopK * T / 4;
+  for (unsigned g = tid; g < E; g += blockDim.x) cnt[g] = 0;
   __syncthreads();
-  for (unsigned i0 = tid; i0 < n4; i0 += kBatch * blockDim.x) {
-    int4 v[kBatch];
+  const int4* ids4 = reinterpret_cast<const int4*>(ids);   // 8T ids: whole int4s
+  const unsigned i0 = blockIdx.x * (chunk_ids / 4), i1 = min(i0 + chunk_ids / 4, routed4);
+  for (unsigned b = i0; b < i1; b += 4 * 256) {
+    int4 v[4];
 #pragma unroll
-    for (unsigned u = 0; u < kBatch; ++u) {
-      const unsigned i = i0 + u * blockDim.x;
-      v[u] = i < n4 ? ids4[i] : int4{-1, -1, -1, -1};
+    for (int u = 0; u < 4; ++u) {
+      const unsigned i = b + tid + 256 * u;
+      v[u] = i < i1 ? ids4[i] : int4{-1, -1, -1, -1};
     }
 #pragma unroll
-    for (unsigned u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < 4; ++u) {
       if (v[u].x >= 0) {
         atomicAdd(&cnt[v[u].x], 1);
         atomicAdd(&cnt[v[u].y], 1);
@@ -209,13 +219,39 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
     }
   }
   __syncthreads();
+  for (unsigned g = tid; g < E; g += blockDim.x) hist[(size_t)g * n_chunks + blockIdx.x] = cnt[g];
+}
+
+// 4b. one workgroup: group totals, row / tile offsets (one-wave scans), tile
+// table, padding, shared-expert rows, and hist turned into each chunk's
+// first row per group.
+__global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, unsigned n_chunks,
+                                                        int* __restrict__ hist,
+                                                        int4* __restrict__ meta,
+                                                        int* __restrict__ sorted) {
+  __shared__ int cnt[kMoeMaxExperts + 1];
+  __shared__ int row_off[kMoeMaxExperts + 2];
+  __shared__ int tile_off[kMoeMaxExperts + 2];
+  const unsigned G = E + 1, tid = threadIdx.x, routed = kMoeTopK * T;
+  // totals: 4 threads per group, each summing a quarter of the chunks
+  {
+    const unsigned g = tid >> 2, part = tid & 3;
+    int sum = 0;
+    if (g < E)
+      for (unsigned c = part; c < n_chunks; c += 4) sum += hist[(size_t)g * n_chunks + c];
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (g < E && part == 0) cnt[g] = sum;
+    if (tid == 0) cnt[E] = (int)T;
+  }
+  __syncthreads();
   if (tid < 64) {   // one wave: exclusive scans of padded rows and tiles per group
     constexpr int kPer = (kMoeMaxExperts + 1 + 63) / 64;   // 5 groups per lane
     int rows[kPer], tiles[kPer], rsum = 0, tsum = 0;
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
       const unsigned g = tid * kPer + j;
-      const int c = g < E ? cnt[g] : (g == E ? (int)T : 0);
+      const int c = g < G ? cnt[g] : 0;
       rows[j] = (c + kPfPad - 1) / kPfPad * kPfPad;
       tiles[j] = (c + kPfBM - 1) / kPfBM;
       rsum += rows[j];
@@ -242,37 +278,66 @@ __global__ __launch_bounds__(1024) void moe_align_kernel(
       toff += tiles[j];
     }
     if (tid == 63) meta[0] = int4{tincl, 0, 0, 0};
-    if (tid == 0) cnt[E] = (int)T;
   }
   __syncthreads();
   for (unsigned g = tid; g < G; g += blockDim.x) {
     const int c = cnt[g], r0 = row_off[g];
-    wpos[g] = r0;
     for (int j = 0; j < tile_off[g + 1] - tile_off[g]; ++j)
       meta[1 + tile_off[g] + j] = int4{(int)g, r0 + kPfBM * j, min(kPfBM, c - kPfBM * j), 0};
     for (int p = r0 + c; p < row_off[g + 1]; ++p) sorted[p] = -1;
   }
-  __syncthreads();
-  for (unsigned i0 = tid; i0 < n4; i0 += kBatch * blockDim.x) {
-    int4 v[kBatch];
+  {   // chunk bases: one wave per group, exclusive prefix over the chunks
+    const unsigned wave = tid >> 6, lane = tid & 63;
+    for (unsigned g = wave; g < E; g += blockDim.x / 64) {
+      int run = row_off[g];
+      for (unsigned c0 = 0; c0 < n_chunks; c0 += 64) {
+        const unsigned ch = c0 + lane;
+        const int n = ch < n_chunks ? hist[(size_t)g * n_chunks + ch] : 0;
+        int incl = n;
 #pragma unroll
-    for (unsigned u = 0; u < kBatch; ++u) {
-      const unsigned i = i0 + u * blockDim.x;
-      v[u] = i < n4 ? ids4[i] : int4{-1, -1, -1, -1};
-    }
-#pragma unroll
-    for (unsigned u = 0; u < kBatch; ++u) {
-      if (v[u].x >= 0) {
-        const int i = 4 * (int)(i0 + u * blockDim.x);
-        sorted[atomicAdd(&wpos[v[u].x], 1)] = i;
-        sorted[atomicAdd(&wpos[v[u].y], 1)] = i + 1;
-        sorted[atomicAdd(&wpos[v[u].z], 1)] = i + 2;
-        sorted[atomicAdd(&wpos[v[u].w], 1)] = i + 3;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int up = __shfl_up(incl, o, 64);
+          if ((int)lane >= o) incl += up;
+        }
+        if (ch < n_chunks) hist[(size_t)g * n_chunks + ch] = run + incl - n;
+        run += __shfl(incl, 63, 64);
       }
     }
   }
   const int shared0 = row_off[E];
   for (unsigned t = tid; t < T; t += blockDim.x) sorted[shared0 + t] = (int)(routed + t);
+}
+
+// 4c. per-chunk scatter: slot i goes to its group's next row of this chunk.
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const int* __restrict__ ids, unsigned T,
+                                                          unsigned E, unsigned n_chunks,
+                                                          unsigned chunk_ids,
+                                                          const int* __restrict__ base,
+                                                          int* __restrict__ sorted) {
+  __shared__ int pos[kMoeMaxExperts];
+  const unsigned tid = threadIdx.x, routed4 = kMoeTopK * T / 4;
+  for (unsigned g = tid; g < E; g += blockDim.x) pos[g] = base[(size_t)g * n_chunks + blockIdx.x];
+  __syncthreads();
+  const int4* ids4 = reinterpret_cast<const int4*>(ids);
+  const unsigned i0 = blockIdx.x * (chunk_ids / 4), i1 = min(i0 + chunk_ids / 4, routed4);
+  for (unsigned b = i0; b < i1; b += 4 * 256) {
+    int4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const unsigned i = b + tid + 256 * u;
+      v[u] = i < i1 ? ids4[i] : int4{-1, -1, -1, -1};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (v[u].x >= 0) {
+        const int i = (int)(4 * (b + tid + 256 * u));
+        sorted[atomicAdd(&pos[v[u].x], 1)] = i;
+        sorted[atomicAdd(&pos[v[u].y], 1)] = i + 1;
+        sorted[atomicAdd(&pos[v[u].z], 1)] = i + 2;
+        sorted[atomicAdd(&pos[v[u].w], 1)] = i + 3;
+      }
+    }
+  }
 }
 
 // ---- 2/5/6. grouped GEMM ----------------------------------------------------
@@ -633,7 +698,13 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
 
   hipLaunchKernelGGL(moe_topk_kernel, dim3(tok_blocks), dim3(256), 0, st, logits,
                      L.ld_logits, E, T, ids, rw, sgw);
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), 0, st, ids, T, E, meta, sorted);
+  int* hist = reinterpret_cast<int*>(ws + L.hist);
+  hipLaunchKernelGGL(moe_hist_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E, L.n_chunks,
+                     L.chunk_ids, hist);
+  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, T, E, L.n_chunks, hist, meta,
+                     sorted);
+  hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E,
+                     L.n_chunks, L.chunk_ids, hist, sorted);
 
   g.a = h2;
   g.w = static_cast<const bf16*>(expert_gate_up);

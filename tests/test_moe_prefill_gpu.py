@@ -104,3 +104,28 @@ def test_moe_prefill_8192_tokens_sampled_rows(gpu):
     ref = O.moe_block(inp[rows], attn[rows], w, forced_ids=ids[rows], grouped=True)
     assert (out[rows].float() - ref.float()).abs().max().item() <= TOL
 
+
+
+def test_moe_prefill_max_tokens_sampled_rows(gpu):
+    """T = 262144, the largest accepted (alignment chunks capped, so each
+    histogram workgroup covers 8192 ids): inputs drawn on the device, every
+    output finite, sampled rows against the oracle."""
+    from qwen36_attn.moe import MoEBlock
+    g = syn.gen(630)
+    w = syn.moe_weights(g, n_experts=256)
+    t = 262144
+    gd = torch.Generator(device=gpu).manual_seed(631)
+    inp = (torch.randn(t, 2048, generator=gd, device=gpu) * 0.5).to(torch.bfloat16)
+    attn = (torch.randn(t, 2048, generator=gd, device=gpu) * 0.5).to(torch.bfloat16)
+    block = MoEBlock({k: v.to(gpu) for k, v in w.items()})
+    print("moe prefill T=262144", flush=True)
+    out, ids, rw, logits, _ = block.prefill(inp, attn, debug=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all().item()
+    rows = torch.tensor([0, 1, 4095, 4096, 131071, 200000, t - 2, t - 1])
+    ids_r, rw_r, lg_r = ids[rows].cpu(), rw[rows].cpu(), logits[rows].cpu().float()
+    _check_routing(ids_r, rw_r, lg_r, 256)
+    ref = O.moe_block(inp[rows].cpu(), attn[rows].cpu(), w, forced_ids=ids_r, grouped=True)
+    assert (out[rows].cpu().float() - ref.float()).abs().max().item() <= TOL
+    del inp, attn, out, block
+    torch.cuda.empty_cache()
