@@ -287,8 +287,28 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, 
     for (int p = r0 + c; p < row_off[g + 1]; ++p) sorted[p] = -1;
   }
   {   // chunk bases: one wave per group, exclusive prefix over the chunks
-    const unsigned wave = tid >> 6, lane = tid & 63;
-    for (unsigned g = wave; g < E; g += blockDim.x / 64) {
+    const unsigned wave = tid >> 6, lane = tid & 63, waves = blockDim.x / 64;
+    if (n_chunks <= 64) {   // every group's counts loaded up front (one round trip)
+      constexpr int kGpw = (kMoeMaxExperts + 15) / 16;   // groups per wave (16 waves)
+      int n[kGpw];
+#pragma unroll
+      for (int j = 0; j < kGpw; ++j) {
+        const unsigned g = wave + waves * j;
+        n[j] = (g < E && lane < n_chunks) ? hist[(size_t)g * n_chunks + lane] : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < kGpw; ++j) {
+        const unsigned g = wave + waves * j;
+        int incl = n[j];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int up = __shfl_up(incl, o, 64);
+          if ((int)lane >= o) incl += up;
+        }
+        if (g < E && lane < n_chunks) hist[(size_t)g * n_chunks + lane] = row_off[g] + incl - n[j];
+      }
+    } else
+    for (unsigned g = wave; g < E; g += waves) {
       int run = row_off[g];
       for (unsigned c0 = 0; c0 < n_chunks; c0 += 64) {
         const unsigned ch = c0 + lane;
