@@ -482,10 +482,11 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
     brs = buffer_rsrc(wg, (unsigned)kMoeHidden * kMoeInter * 2u);
   }
 
-  // Fetch plan: one instruction moves 8 rows of 128 bytes (lane = row in the
-  // 8 x chunk position; the source chunk is position ^ row, so LDS holds the
-  // swizzled layout).  A instructions whose rows are all past the tile's rows
-  // are skipped.
+  // Fetch plan: one instruction moves 1 KiB, kPfRpi rows of kPfRowB bytes
+  // (lane = row in the instruction x chunk position; the source chunk is
+  // position ^ key(row), so LDS holds the swizzled layout).  A instructions
+  // whose rows are all past the tile's rows load nothing (an out-of-range
+  // offset), which keeps every wave's count of loads per stage equal.
   const int rin = lane / kPfCpr, cpos = lane % kPfCpr;   // row in the instruction, chunk
   unsigned f_off[kPfInstr];
   u32x4 f_rs[kPfInstr];
@@ -531,8 +532,9 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
     const unsigned kb = (unsigned)step * kPfRowB;
 #pragma unroll
     for (int j = 0; j < kPfInstr; ++j) {
-      // a skipped instruction is replaced by a dummy in-range load so that
-      // every wave keeps the same count of outstanding loads per stage
+      // a dead instruction is still issued, with an out-of-range offset (no
+      // memory is read), so every wave keeps the same count of outstanding
+      // loads per stage for the vmcnt waits
       const int ins = wave * kPfInstr + j;
       fetch_rows(sbase + ins * kPfRpi * kPfRowB, f_live[j] ? (int)(f_off[j] + kb) : (int)kOob,
                  f_rs[j]);
