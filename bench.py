@@ -44,7 +44,7 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
-    p.add_argument("--only", choices=["decode", "prefill", "gdn", "moe", "copy"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "gdn", "moe", "moe_decode", "copy"], default=None,
                    help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
 
@@ -545,6 +545,8 @@ def run_only(torch, fa, dev, args):
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
     elif args.only == "moe":
         r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup)]
+    elif args.only == "moe_decode":
+        r = [bench_moe_decode(torch, dev, 40, args.steps, args.warmup, False)]
     else:
         x = torch.empty(64 * 1024 * 1024, dtype=torch.float32, device=dev)
         x.fill_(1.0)
