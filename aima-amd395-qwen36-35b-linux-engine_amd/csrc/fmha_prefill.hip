@@ -13,7 +13,8 @@
 //  * workgroup = 8 waves = 256 query rows of one head; wave = 32 rows; one
 //    workgroup per CU (two waves per SIMD) shares each staged K/V tile
 //    among 256 rows (measured 5-7% faster than two 4-wave workgroups per
-//    CU, which stage every tile twice).
+//    CU, which stage every tile twice).  Short square prompts (fewer than
+//    256 such workgroups) use 4- or 2-wave workgroups (128 or 64 rows).
 //  * per 32-key tile: K and V are staged in LDS (padded row-pair blocks, so
 //    every LDS address is a per-lane base plus an immediate); S^T = K Q^T on
 //    v_mfma_f32_32x32x16_bf16 (A = K from LDS, B = Q^T held in registers for
@@ -36,9 +37,7 @@
 namespace q36 {
 namespace {
 
-constexpr int kFmWaves = 8;
 constexpr int kFmRowsPerWave = 32;
-constexpr int kFmRows = kFmWaves * kFmRowsPerWave;   // 256
 constexpr int kFmKv = 32;                             // keys per tile
 constexpr int kRowBytes = kD * 2;                     // 512
 constexpr int kTokBytes = kHkv * kD * 2;              // 1024: one cache row
@@ -55,15 +54,17 @@ constexpr int kKTile = 16 * kKBlk;                    // 16640
 constexpr int kVTile = 16 * kVBlk;                    // 17408
 constexpr int kFmStage = kKTile + kVTile;             // 34048
 constexpr int kFmLds = 2 * kFmStage;                  // 68096: double buffer
-constexpr int kFmLoadsPerWave = 16 / kFmWaves;        // 2 blocks per wave
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+template <int kFmWaves>
 __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, float* __restrict__ out, unsigned q_tokens,
     unsigned kv_tokens, unsigned n_qtiles) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
+  constexpr int kFmRows = kFmWaves * kFmRowsPerWave;
+  constexpr int kFmLoadsPerWave = 16 / kFmWaves;       // 16 row-pair blocks per tile
 
   // XCD-aware tile mapping (see header).
   const unsigned b = blockIdx.x;
@@ -236,17 +237,35 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
     return Q36_EINVAL;
   static bool attr_set = false;
   if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(fmha_prefill_kernel),
-        hipFuncAttributeMaxDynamicSharedMemorySize, kFmLds);
-    if (e != hipSuccess) return (int)e;
+    for (const void* f : {reinterpret_cast<const void*>(fmha_prefill_kernel<8>),
+                          reinterpret_cast<const void*>(fmha_prefill_kernel<4>),
+                          reinterpret_cast<const void*>(fmha_prefill_kernel<2>)}) {
+      const hipError_t e =
+          hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFmLds);
+      if (e != hipSuccess) return (int)e;
+    }
     attr_set = true;
   }
-  const unsigned n_qtiles = (q_tokens + kFmRows - 1) / kFmRows;
-  hipLaunchKernelGGL(fmha_prefill_kernel, dim3(n_qtiles * kHq), dim3(64 * kFmWaves), kFmLds,
-                     stream, static_cast<const bf16*>(q),
-                     static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                     out, q_tokens, kv_tokens, n_qtiles);
+  // Query rows per workgroup: 256 (8 waves) when that gives at least 256
+  // workgroups or the rows extend a cached prefix (long rows); short square
+  // prompts use 128 or 64 rows so they still spread over the CUs (measured on
+  // MI355X: T = 1024 51 vs 54 us, T = 2048 96 vs 97-102 us; 8 waves stay best
+  // from T = 4096 and for 1024 rows over a 4096-token prefix).
+  auto tiles = [&](unsigned rows) { return (q_tokens + rows - 1) / rows; };
+  const bf16* qb = static_cast<const bf16*>(q);
+  if (tiles(256) * kHq >= 256u || kv_tokens > q_tokens) {
+    hipLaunchKernelGGL(fmha_prefill_kernel<8>, dim3(tiles(256) * kHq), dim3(512), kFmLds,
+                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                       out, q_tokens, kv_tokens, tiles(256));
+  } else if (tiles(128) * kHq >= 256u) {
+    hipLaunchKernelGGL(fmha_prefill_kernel<4>, dim3(tiles(128) * kHq), dim3(256), kFmLds,
+                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                       out, q_tokens, kv_tokens, tiles(128));
+  } else {
+    hipLaunchKernelGGL(fmha_prefill_kernel<2>, dim3(tiles(64) * kHq), dim3(128), kFmLds,
+                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                       out, q_tokens, kv_tokens, tiles(64));
+  }
   return static_cast<int>(hipGetLastError());
 }
 
