@@ -34,6 +34,8 @@
 //    heaviest (latest) causal tiles first.
 #include "common.h"
 
+#include <mutex>
+
 namespace q36 {
 namespace {
 
@@ -57,21 +59,39 @@ constexpr int kFmLds = 2 * kFmStage;                  // 68096: double buffer
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int kFmWaves>
+// Split-K partials (kSplit): workgroup (q tile, chunk, head) writes its
+// unnormalised O rows and (m, l) for keys [chunk * chunk_keys, +chunk_keys).
+struct SplitArgs {
+  float* o;             // [tile][chunk][head][256 rows][256]
+  float* ml;            // [tile][chunk][head][256 rows][2]
+  unsigned chunk_keys;  // multiple of 32
+  unsigned n_chunks;
+};
+
+template <int kFmWaves, bool kSplit>
 __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, float* __restrict__ out, unsigned q_tokens,
-    unsigned kv_tokens, unsigned n_qtiles) {
+    unsigned kv_tokens, unsigned n_qtiles, SplitArgs sp) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int kFmRows = kFmWaves * kFmRowsPerWave;
   constexpr int kFmLoadsPerWave = 16 / kFmWaves;       // 16 row-pair blocks per tile
 
-  // XCD-aware tile mapping (see header).
+  // XCD-aware tile mapping (see header); split: (tile, chunk, head).
   const unsigned b = blockIdx.x;
-  const unsigned xcd = b & 7u, n = b >> 3;
-  const int kvh = xcd >> 2;
-  const int head = kvh * kGroup + (xcd & 3) * 2 + (n & 1);
-  const unsigned qtile = n_qtiles - 1 - (n >> 1);
+  int kvh, head;
+  unsigned qtile, chunk = 0;
+  if constexpr (kSplit) {
+    head = (int)(b % kHq);
+    kvh = head / kGroup;
+    qtile = (b / kHq) / sp.n_chunks;
+    chunk = (b / kHq) % sp.n_chunks;
+  } else {
+    const unsigned xcd = b & 7u, n = b >> 3;
+    kvh = xcd >> 2;
+    head = kvh * kGroup + (xcd & 3) * 2 + (n & 1);
+    qtile = n_qtiles - 1 - (n >> 1);
+  }
   const unsigned q0 = qtile * kFmRows;
 
   const int tid = threadIdx.x;
@@ -86,6 +106,10 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
   const unsigned wave_lim =
       min(wave_first + kFmRowsPerWave - 1, q_tokens - 1) + off;
   const unsigned kv_end = min(kv_tokens, min(q0 + kFmRows, q_tokens) + off);
+  // key range of this workgroup: whole rows, or one chunk of them
+  const unsigned kv_first = kSplit ? chunk * sp.chunk_keys : 0u;
+  const unsigned kv_stop = kSplit ? min(kv_end, kv_first + sp.chunk_keys) : kv_end;
+  if (kSplit && kv_first >= kv_end) return;   // past the tile's last key
 
   // Q^T operand: step s covers dims s*16 + 8*lg .. +8 of this lane's row.
   bf16x8 qf[16];
@@ -136,9 +160,10 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
   const int vx = 4 * lg + (m16 >> 2);
   const int vbase = vx * kVBlk + 32 * (grp & 1) + 8 * (m16 & 3);
 
-  const unsigned n_tiles = (kv_end + kFmKv - 1) / kFmKv;
-  fetch(0, 0);
-  for (unsigned t = 0; t < n_tiles; ++t) {
+  const unsigned t_first = kv_first / kFmKv;
+  const unsigned n_tiles = (kv_stop + kFmKv - 1) / kFmKv;
+  fetch(kv_first, t_first & 1);
+  for (unsigned t = t_first; t < n_tiles; ++t) {
     const unsigned kv0 = t * kFmKv;
     const int stage = t & 1;
     __builtin_amdgcn_s_waitcnt(0);   // this wave's fetches of tile t landed
@@ -176,7 +201,12 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
       mx = wave_max_xor(mx, 32);
       return mx * scale;
     };
-    if (t == 0) m = row_max();
+    if (t == t_first) {
+      // a row whose keys all precede this chunk sees only masked scores in
+      // its first tile (and in every later one): any finite m keeps p = 0
+      m = row_max();
+      if (kSplit && m == -INFINITY) m = 0.f;
+    }
     float psum = 0.f;
     bf16x8 pb[2];
 #pragma unroll
@@ -216,6 +246,19 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
   }
   l += __shfl_xor(l, 32, 64);
   if (!row_valid) return;
+  if constexpr (kSplit) {
+    const size_t item = ((size_t)qtile * sp.n_chunks + chunk) * kHq + head;
+    const unsigned r = row - q0;
+    float* op = sp.o + (item * kFmRows + r) * kD + 4 * lg;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<f32x4*>(op + dt * 32 + 8 * r4) =
+            f32x4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
+    if (lg == 0) *reinterpret_cast<float2*>(sp.ml + (item * kFmRows + r) * 2) = float2{m, l};
+    return;
+  }
   const float inv = 1.0f / l;
   float* op = out + (size_t)row * kQDim + head * kD + 4 * lg;
 #pragma unroll
@@ -229,6 +272,66 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
   }
 }
 
+// Split-K combine: thread (row, 8 dims) of (q tile, head) merges the live
+// chunks' partials: M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c -
+// M) / L (chunks where the row saw no key have l = 0 and weigh nothing).
+// grid = tiles x 16 heads x 16 row groups; block = 512 (16 rows x 32 dims/8).
+__global__ __launch_bounds__(512) void fmha_split_combine_kernel(
+    const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
+    unsigned q_tokens, unsigned kv_tokens, unsigned chunk_keys, unsigned n_chunks) {
+  constexpr int kRows = 256;
+  const unsigned rg = blockIdx.x % 16, head = (blockIdx.x / 16) % kHq, qtile = blockIdx.x / (16 * kHq);
+  const unsigned r = rg * 16 + (threadIdx.x >> 5);
+  const unsigned row = qtile * kRows + r;
+  if (row >= q_tokens) return;
+  const int d0 = 8 * (threadIdx.x & 31);
+  const unsigned off = kv_tokens - q_tokens;
+  const unsigned kv_end = min(kv_tokens, min(qtile * kRows + kRows, q_tokens) + off);
+  const unsigned live = (kv_end + chunk_keys - 1) / chunk_keys;
+  float M = -INFINITY;
+  for (unsigned c = 0; c < live; ++c) {
+    const size_t item = ((size_t)qtile * n_chunks + c) * kHq + head;
+    const float2 ml = *reinterpret_cast<const float2*>(pml + (item * kRows + r) * 2);
+    if (ml.y > 0.f) M = fmaxf(M, ml.x);
+  }
+  float L = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (unsigned c = 0; c < live; ++c) {
+    const size_t item = ((size_t)qtile * n_chunks + c) * kHq + head;
+    const float2 ml = *reinterpret_cast<const float2*>(pml + (item * kRows + r) * 2);
+    if (!(ml.y > 0.f)) continue;
+    const float w = __builtin_amdgcn_exp2f(ml.x - M);
+    L += w * ml.y;
+    const f32x4* src = reinterpret_cast<const f32x4*>(po + (item * kRows + r) * kD + d0);
+    const f32x4 a = src[0], b = src[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[e] += w * a[e];
+      acc[4 + e] += w * b[e];
+    }
+  }
+  const float inv = 1.0f / L;
+  f32x4* dst = reinterpret_cast<f32x4*>(out + (size_t)row * kQDim + head * kD + d0);
+  dst[0] = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+  dst[1] = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+}
+
+// Provider-owned split-K scratch (qrt_ck_fmha_prepare allocates it on the
+// current device; kept until the process ends): room for kSplitItems
+// (tile, chunk, head) partials of 256 rows.  Launches without it, or whose
+// split would not fit, run unsplit.  Launches that use it share it, so they
+// must be ordered (one stream, as the reference's engine launches them).
+constexpr unsigned kSplitItems = 512;
+constexpr size_t kSplitItemBytes = (size_t)256 * (kD + 2) * sizeof(float);
+std::mutex g_fm_mutex;
+void* g_fm_scratch[64] = {};
+
+void* split_scratch_for_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_fm_mutex);
+  return g_fm_scratch[dev];
+}
+
 int launch_fmha(const void* q, const void* k, const void* v, float* out,
                 unsigned q_tokens, unsigned kv_tokens, hipStream_t stream) {
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
@@ -237,34 +340,56 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
     return Q36_EINVAL;
   static bool attr_set = false;
   if (!attr_set) {
-    for (const void* f : {reinterpret_cast<const void*>(fmha_prefill_kernel<8>),
-                          reinterpret_cast<const void*>(fmha_prefill_kernel<4>),
-                          reinterpret_cast<const void*>(fmha_prefill_kernel<2>)}) {
+    for (const void* f : {reinterpret_cast<const void*>(fmha_prefill_kernel<8, false>),
+                          reinterpret_cast<const void*>(fmha_prefill_kernel<4, false>),
+                          reinterpret_cast<const void*>(fmha_prefill_kernel<2, false>),
+                          reinterpret_cast<const void*>(fmha_prefill_kernel<8, true>)}) {
       const hipError_t e =
           hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFmLds);
       if (e != hipSuccess) return (int)e;
     }
     attr_set = true;
   }
+  auto tiles = [&](unsigned rows) { return (q_tokens + rows - 1) / rows; };
+  const bf16* qb = static_cast<const bf16*>(q);
+  const bf16* kb = static_cast<const bf16*>(k);
+  const bf16* vb = static_cast<const bf16*>(v);
+  const SplitArgs none{nullptr, nullptr, 0u, 1u};
+  // Too few 256-row tiles to fill the GPU: split each tile's key range into
+  // chunks (about 256 live workgroups) when the provider scratch is there.
+  if (tiles(256) * kHq < 256u) {
+    const unsigned n_chunks = (256u + tiles(256) * kHq - 1) / (tiles(256) * kHq);
+    const unsigned chunk_keys = (((kv_tokens + n_chunks - 1) / n_chunks) + kFmKv - 1) /
+                                kFmKv * kFmKv;
+    void* scratch = split_scratch_for_current_device();
+    if (n_chunks > 1 && scratch != nullptr && tiles(256) * n_chunks * kHq <= kSplitItems) {
+      SplitArgs sp;
+      sp.o = static_cast<float*>(scratch);
+      sp.ml = sp.o + (size_t)kSplitItems * 256 * kD;
+      sp.chunk_keys = chunk_keys;
+      sp.n_chunks = n_chunks;
+      hipLaunchKernelGGL((fmha_prefill_kernel<8, true>), dim3(tiles(256) * n_chunks * kHq),
+                         dim3(512), kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens,
+                         tiles(256), sp);
+      hipLaunchKernelGGL(fmha_split_combine_kernel, dim3(tiles(256) * kHq * 16), dim3(512), 0,
+                         stream, sp.o, sp.ml, out, q_tokens, kv_tokens, chunk_keys, n_chunks);
+      return static_cast<int>(hipGetLastError());
+    }
+  }
   // Query rows per workgroup: 256 (8 waves) when that gives at least 256
   // workgroups or the rows extend a cached prefix (long rows); short square
   // prompts use 128 or 64 rows so they still spread over the CUs (measured on
   // MI355X: T = 1024 51 vs 54 us, T = 2048 96 vs 97-102 us; 8 waves stay best
   // from T = 4096 and for 1024 rows over a 4096-token prefix).
-  auto tiles = [&](unsigned rows) { return (q_tokens + rows - 1) / rows; };
-  const bf16* qb = static_cast<const bf16*>(q);
   if (tiles(256) * kHq >= 256u || kv_tokens > q_tokens) {
-    hipLaunchKernelGGL(fmha_prefill_kernel<8>, dim3(tiles(256) * kHq), dim3(512), kFmLds,
-                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                       out, q_tokens, kv_tokens, tiles(256));
+    hipLaunchKernelGGL((fmha_prefill_kernel<8, false>), dim3(tiles(256) * kHq), dim3(512),
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), none);
   } else if (tiles(128) * kHq >= 256u) {
-    hipLaunchKernelGGL(fmha_prefill_kernel<4>, dim3(tiles(128) * kHq), dim3(256), kFmLds,
-                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                       out, q_tokens, kv_tokens, tiles(128));
+    hipLaunchKernelGGL((fmha_prefill_kernel<4, false>), dim3(tiles(128) * kHq), dim3(256),
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(128), none);
   } else {
-    hipLaunchKernelGGL(fmha_prefill_kernel<2>, dim3(tiles(64) * kHq), dim3(128), kFmLds,
-                       stream, qb, static_cast<const bf16*>(k), static_cast<const bf16*>(v),
-                       out, q_tokens, kv_tokens, tiles(64));
+    hipLaunchKernelGGL((fmha_prefill_kernel<2, false>), dim3(tiles(64) * kHq), dim3(128),
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(64), none);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -273,10 +398,25 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
 }  // namespace q36
 
 // ---- provider ABI ---------------------------------------------------------
-// The launch path owns no device memory, so prepare/release only validate.
+// prepare allocates the split-K scratch on the current device (once, 132 MiB);
+// it stays allocated until the process ends -- a graph captured with a split
+// launch holds its address -- so release has nothing to free.
 
 Q36_EXPORT int qrt_ck_fmha_prepare(unsigned tokens) {
-  return (tokens > 0u && tokens <= q36::kMaxTokens) ? Q36_OK : Q36_EINVAL;
+  if (tokens == 0u || tokens > q36::kMaxTokens) return Q36_EINVAL;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= 64) return Q36_EINVAL;
+  std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
+  if (q36::g_fm_scratch[dev] == nullptr) {
+    e = hipMalloc(&q36::g_fm_scratch[dev], q36::kSplitItems * q36::kSplitItemBytes);
+    if (e != hipSuccess) {
+      q36::g_fm_scratch[dev] = nullptr;
+      return (int)e;
+    }
+  }
+  return Q36_OK;
 }
 
 Q36_EXPORT int qrt_ck_fmha_bf16_launch(const void* q, const void* k,

@@ -144,9 +144,24 @@ def fmha_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out is None:
         out = torch.empty(t, Q_DIM, dtype=torch.float32, device=q.device)
     require(out, "out", torch.float32, shape=(t, Q_DIM))
+    _prepare_provider(q.device)
     _lib.call("qrt_ck_fmha_bf16_launch_ex", ptr(q), ptr(k), ptr(v), ptr(out), t, s,
               stream_handle(q.device))
     return out
+
+
+_PREPARED: set = set()
+
+
+def _prepare_provider(device: torch.device) -> None:
+    """qrt_ck_fmha_prepare once per device (allocates the provider's split-K
+    scratch, which short prompts use; it is kept for the process)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx in _PREPARED:
+        return
+    with torch.cuda.device(idx):
+        _lib.call("qrt_ck_fmha_prepare", MAX_TOKENS)
+    _PREPARED.add(idx)
 
 
 class FmhaProvider:

@@ -33,7 +33,14 @@ extern "C" {
  * Q [q_tokens,16,256] bf16, K/V [kv_tokens,2,256] bf16, out fp32
  * [q_tokens,4096]; scale 1/16; top-left causal mask when
  * q_tokens == kv_tokens, bottom-right otherwise. */
-int qrt_ck_fmha_prepare(unsigned tokens); /* 0 < tokens <= 262144 */
+/* prepare (0 < tokens <= 262144) allocates, once per device, the provider's
+ * 132 MiB split-K scratch: launches with fewer than 16 query tiles of 256
+ * rows split each tile's key range over several workgroups plus a combine
+ * launch and use it (without it they run unsplit).  Launches that use it must
+ * be ordered (one stream).  The scratch is kept until the process ends
+ * (graphs captured with a split launch hold its address), so release has
+ * nothing to free. */
+int qrt_ck_fmha_prepare(unsigned tokens);
 int qrt_ck_fmha_bf16_launch(const void* q, const void* k, const void* v,
                             float* out, unsigned tokens, void* stream);
 int qrt_ck_fmha_bf16_launch_ex(const void* q, const void* k, const void* v,

@@ -67,17 +67,23 @@ def test_prefill_8k_causal_sampled_rows(gpu):
     assert torch.isfinite(got).all()
 
 
-def test_prefix_extension_equals_tail_of_full_prefill(gpu):
+@pytest.mark.parametrize("s,t,tol", [
+    # short: both launches split the key range, in different chunks, so P is
+    # rounded to bf16 against different per-chunk reference maxima
+    (1500, 700, TOL_TIGHT),
+    # long, tile-aligned: both launches run the same unsplit 256-row tiles
+    (8192, 4096, 1e-6)])
+def test_prefix_extension_equals_tail_of_full_prefill(gpu, s, t, tol):
     """Bottom-right prefill over S equals the last T rows of a full causal
     prefill over S (prefix-cache continuation)."""
     from qwen36_attn.full_attention import fmha_prefill
-    s, t = 1500, 700
     q, k, v = _inputs(s, s, seed=21)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    print(f"prefill prefix extension S={s} T={t}", flush=True)
     full = fmha_prefill(qd, kd, vd)
     tail = fmha_prefill(qd[s - t:].contiguous(), kd, vd)
     torch.cuda.synchronize()
-    assert (full[s - t:] - tail).abs().max().item() <= 1e-6
+    assert (full[s - t:] - tail).abs().max().item() <= tol
 
 
 def test_provider_mirror_and_errors(gpu):
