@@ -402,19 +402,21 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
 // it stays allocated until the process ends -- a graph captured with a split
 // launch holds its address -- so release has nothing to free.
 
+// Returns 0 for a valid token count, hipErrorInvalidValue otherwise (the
+// reference's contract); if the scratch cannot be allocated (no device, out
+// of memory) the provider simply stays without it and launches run unsplit.
 Q36_EXPORT int qrt_ck_fmha_prepare(unsigned tokens) {
   if (tokens == 0u || tokens > q36::kMaxTokens) return Q36_EINVAL;
   int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return (int)e;
-  if (dev < 0 || dev >= 64) return Q36_EINVAL;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return Q36_OK;
+  }
   std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
-  if (q36::g_fm_scratch[dev] == nullptr) {
-    e = hipMalloc(&q36::g_fm_scratch[dev], q36::kSplitItems * q36::kSplitItemBytes);
-    if (e != hipSuccess) {
-      q36::g_fm_scratch[dev] = nullptr;
-      return (int)e;
-    }
+  if (q36::g_fm_scratch[dev] == nullptr &&
+      hipMalloc(&q36::g_fm_scratch[dev], q36::kSplitItems * q36::kSplitItemBytes) != hipSuccess) {
+    q36::g_fm_scratch[dev] = nullptr;
+    (void)hipGetLastError();
   }
   return Q36_OK;
 }

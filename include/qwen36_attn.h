@@ -36,7 +36,8 @@ extern "C" {
 /* prepare (0 < tokens <= 262144) allocates, once per device, the provider's
  * 132 MiB split-K scratch: launches with fewer than 16 query tiles of 256
  * rows split each tile's key range over several workgroups plus a combine
- * launch and use it (without it they run unsplit).  Launches that use it must
+ * launch and use it (without it -- not prepared, or the allocation failed, in
+ * which case prepare still returns 0 -- they run unsplit).  Launches that use it must
  * be ordered (one stream).  The scratch is kept until the process ends
  * (graphs captured with a split launch hold its address), so release has
  * nothing to free. */
