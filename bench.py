@@ -486,6 +486,35 @@ def bench_gdn_decode_step(torch, dev, layers, iters, warmup, use_graph, fused=Tr
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_config1_layers(torch, dev, t, iters, warmup, seed=12):
+    """Config 1: one gated full-attention layer and one Gated-DeltaNet layer
+    (random weights of the model's shapes) prefilling T tokens from an empty
+    cache / zero state -- projections through torch (hipBLASLt), attention,
+    norms and the GDN core through this library -- and one decode step of
+    each after the prompt (the native one-token path: fused projection
+    GEMVs, fused step kernels).  Times are per layer call."""
+    from qwen36_attn import synthetic as syn
+    from qwen36_attn.full_attention import FullAttentionLayer
+    from qwen36_attn.gated_deltanet import LinearAttentionLayer
+    g = syn.gen(seed)
+    wf = {k: v.to(dev) for k, v in syn.full_attention_weights(g).items()}
+    wl = {k: v.to(dev) for k, v in syn.linear_attention_weights(g, a_max=1.0).items()}
+    fl = FullAttentionLayer(wf, t + 64, dev)
+    ll = LinearAttentionLayer(wl, dev)
+    x = syn.randn((t, 2048), g, 0.5).to(dev)
+    x1 = syn.randn((1, 2048), g, 0.5).to(dev)
+    tm = Timer(torch)
+    res = {"tokens": t}
+    res["full_attention_prefill_us"] = tm.time(lambda: fl.forward(x, 0, "prefill"), iters, warmup) * 1000
+    res["linear_attention_prefill_us"] = tm.time(lambda: ll.forward(x, "prefill"), iters, warmup) * 1000
+    fl.forward(x, 0, "prefill")
+    res["full_attention_decode_us"] = tm.time(lambda: fl.forward(x1, t, "decode"), iters, warmup) * 1000
+    res["linear_attention_decode_us"] = tm.time(lambda: ll.forward(x1, "decode"), iters, warmup) * 1000
+    del fl, ll, wf, wl
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_gdn_prefill(torch, dev, t, iters, warmup, seed=3):
     """Config 4: chunked delta-rule prefill of T tokens from zero state."""
     from qwen36_attn import gated_deltanet as G
@@ -597,6 +626,7 @@ def main():
         "gdn_decode_unfused_30layers": bench_gdn_decode_step(torch, dev, GDN_LAYERS, 50, 5,
                                                              use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
+        "config1_layers_1k": bench_config1_layers(torch, dev, 1024, 20, 3),
         "moe_prefill_8k": bench_moe_prefill(torch, dev, 8192, 10, 2),
         "moe_prefill_1k": bench_moe_prefill(torch, dev, 1024, 20, 3),
         "moe_prefill_8k_torch_expert_loop": bench_moe_prefill(torch, dev, 8192, 3, 1, native=False),
