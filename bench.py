@@ -567,7 +567,9 @@ def run_only(torch, fa, dev, args):
         r = bench_decode(torch, fa, dev, 131072, N_FULL_LAYERS, args.steps, args.warmup, False)
     elif args.only == "prefill":
         r = [bench_prefill(torch, fa, dev, 8192, 8192, args.steps, args.warmup),
-             bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup)]
+             bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup),
+             bench_prefill(torch, fa, dev, 1024, 1024, args.steps, args.warmup),
+             bench_prefill(torch, fa, dev, 1024, 5120, args.steps, args.warmup)]
     elif args.only == "gdn":
         r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
