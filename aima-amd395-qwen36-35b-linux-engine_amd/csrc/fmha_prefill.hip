@@ -21,6 +21,9 @@
 //    the whole kernel), online softmax per row
 //    in fp32 (exp2 domain), O^T += V^T P^T (A = V^T read with
 //    ds_read_b64_tr_b16, B = P^T taken straight from the S^T accumulator).
+//  * LDS operand reads run 4 MFMAs ahead of their use (register rings whose
+//    issue order is pinned by sched_group_barrier), so the dependent QK^T
+//    chain and the PV MFMAs do not wait on LDS latency.
 //  * K/V tiles are fetched straight into LDS (global_load_lds_dwordx4, no
 //    register staging) into a double buffer (64 KiB), so the next tile's
 //    HBM/L2 latency overlaps the current tile's MFMA work; the two waves
@@ -174,10 +177,26 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     const char* vp = lds + stage * kFmStage + kKTile + vbase;
 
     // S^T[key][row] for the 32-key tile.
+    // K operands go through a 4-deep register ring: the read for step st + 4
+    // is issued right after step st's MFMA (the sched_group_barrier sequence
+    // pins that order; left alone, the scheduler keeps only 2 reads in flight
+    // and each MFMA of the dependent chain waits a full LDS latency).
+    bf16x8 kr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const bf16x8*>(kp + i * 32);
     f32x16 s0 = f32x16{};
 #pragma unroll
-    for (int st = 0; st < 16; ++st)
-      s0 = mfma32x32x16(*reinterpret_cast<const bf16x8*>(kp + st * 32), qf[st], s0);
+    for (int st = 0; st < 16; ++st) {
+      s0 = mfma32x32x16(kr[st & 3], qf[st], s0);
+      if (st + 4 < 16) kr[st & 3] = *reinterpret_cast<const bf16x8*>(kp + (st + 4) * 32);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     // Lane holds keys kv0 + 8*(r/4) + 4*lg + r%4 of its row.
     const bool diag = kv0 + kFmKv - 1 > wave_first + off || kv0 + kFmKv > kv_tokens;
     if (diag) {  // wave-uniform: only diagonal / ragged tiles pay for masking
@@ -234,15 +253,27 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
 
     // O^T[d][row] += V^T[d][key] P^T[key][row]; step st reduction slots
     // (lg, e) <-> keys 16st + 4lg + e and +8 for e >= 4.
+    // V^T operands: the same ring, 4 MFMAs (8 transposed reads) deep.
+    i16x4 va[4][2];
+    auto vread = [&](int i, int slot) {
+      const char* p = vp + (i >> 3) * kRowBytes + (i & 7) * 64;
+      va[slot][0] = lds_read_tr16(p);
+      va[slot][1] = lds_read_tr16(p + 8 * kVBlk);
+    };
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+    for (int i = 0; i < 4; ++i) vread(i, i);
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const i16x4 a0 = lds_read_tr16(vp + st * kRowBytes + dt * 64);
-        const i16x4 a1 = lds_read_tr16(vp + st * kRowBytes + 8 * kVBlk + dt * 64);
-        o[dt] = mfma32x32x16(cat_bf16x8(a0, a1), pb[st], o[dt]);
-      }
+    for (int i = 0; i < 16; ++i) {
+      o[i & 7] = mfma32x32x16(cat_bf16x8(va[i & 3][0], va[i & 3][1]), pb[i >> 3], o[i & 7]);
+      if (i + 4 < 16) vread(i + 4, i & 3);
     }
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
   }
   l += __shfl_xor(l, 32, 64);
   if (!row_valid) return;
