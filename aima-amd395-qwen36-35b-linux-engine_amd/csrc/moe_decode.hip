@@ -18,7 +18,8 @@
 // with every bf16 rounding of the eager PyTorch text.
 //
 // Launches (all HBM-bound GEMV shapes, 16-byte nontemporal weight loads):
-//  1. moe_router_kernel: residual add + RMSNorm (every wave recomputes h2 from
+//  1. moe_router_kernel: each wave first requests its 2 weight rows, then
+//     residual add + RMSNorm (every wave recomputes h2 from
 //     the 2048 inputs; block 0 stores `after` and h2), then a GEMV over the
 //     fused rows [router (E) | shared_gate (1) | shared gate_proj (512) |
 //     shared up_proj (512)] -> bf16.
@@ -44,6 +45,9 @@ constexpr size_t kWsAct = kWsRw + kMoeTopK * 4;                   // bf16 [9][51
 constexpr size_t kWsProj = kWsAct + (kMoeTopK + 1) * kMoeInter * 2;   // bf16 [E + 1 + 1024]
 constexpr size_t kWsBytes = kWsProj + (kMoeMaxExperts + 1 + 2 * kMoeInter) * 2;
 
+// Router GEMV rows per wave (launch 1 runs one row group per wave).
+constexpr int kRouterRows = 2;
+
 // GEMV of one row r (K = 2048) with x held as lane l's columns 8l + 512j.
 __device__ __forceinline__ float dot2048(const u32x4 (&wr)[4], const float (&xv)[4][8]) {
   float a = 0.f;
@@ -64,6 +68,22 @@ __global__ __launch_bounds__(256, 2) void moe_router_kernel(
   const int lane = threadIdx.x & 63;
   const unsigned wave_g = blockIdx.x * 4 + (threadIdx.x >> 6);
   const unsigned waves = gridDim.x * 4;
+  // This wave's first weight rows are requested before the RMSNorm prologue,
+  // so their HBM latency overlaps it.
+  u32x4 wr[kRouterRows][4];
+  auto load_rows = [&](unsigned r0) {
+#pragma unroll
+    for (int r = 0; r < kRouterRows; ++r) {
+      const unsigned row = min(r0 + r, n_rows - 1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        wr[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            w_in + (size_t)row * kMoeHidden + 512 * j + 8 * lane));
+    }
+  };
+  unsigned r0 = wave_g * kRouterRows;
+  load_rows(r0);   // rows clamp to n_rows - 1, so a spare wave's loads stay in bounds
+  __builtin_amdgcn_sched_barrier(0);
   // after = bf16(inp + attn); h2 = bf16(after * rsqrt(mean(after^2) + eps) * (w + 1))
   float xa[4][8], ss = 0.f;
 #pragma unroll
@@ -100,25 +120,19 @@ __global__ __launch_bounds__(256, 2) void moe_router_kernel(
     }
   }
   bf16* proj = reinterpret_cast<bf16*>(ws + kWsProj);
-  for (unsigned r0 = wave_g * 4; r0 < n_rows; r0 += waves * 4) {
-    u32x4 wr[4][4];
+  for (; r0 < n_rows; r0 += waves * kRouterRows) {
+    float acc[kRouterRows];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const unsigned row = min(r0 + r, n_rows - 1);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wr[r][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            w_in + (size_t)row * kMoeHidden + 512 * j + 8 * lane));
-    }
-    __builtin_amdgcn_sched_barrier(0);   // keep every weight load in flight before the FMAs
-    float acc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = wave_sum(dot2048(wr[r], xv));
-    if (lane < 4 && r0 + lane < n_rows) {
+    for (int r = 0; r < kRouterRows; ++r) acc[r] = wave_sum(dot2048(wr[r], xv));
+    if (lane < kRouterRows && r0 + lane < n_rows) {
       float v = acc[0];
 #pragma unroll
-      for (int r = 1; r < 4; ++r) v = lane == r ? acc[r] : v;
+      for (int r = 1; r < kRouterRows; ++r) v = lane == r ? acc[r] : v;
       proj[r0 + lane] = f2bf(v);
+    }
+    if (r0 + waves * kRouterRows < n_rows) {
+      load_rows(r0 + waves * kRouterRows);
+      __builtin_amdgcn_sched_barrier(0);   // keep every weight load in flight before the FMAs
     }
   }
 }
@@ -284,7 +298,7 @@ Q36_EXPORT int qwen36_moe_decode(const void* inp, const void* attn_out,
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const unsigned n_in = n_experts + 1 + 2 * kMoeInter;
-  const unsigned groups = (n_in + 3) / 4;
+  const unsigned groups = (n_in + kRouterRows - 1) / kRouterRows;
   hipLaunchKernelGGL(moe_router_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
                      static_cast<const bf16*>(inp), static_cast<const bf16*>(attn_out),
                      static_cast<const bf16*>(post_norm_w), static_cast<const bf16*>(w_in),
