@@ -19,16 +19,16 @@
 //
 // Launches (all HBM-bound GEMV shapes, 16-byte nontemporal weight loads):
 //  1. moe_router_kernel: each wave first requests its 2 weight rows, then
-//     residual add + RMSNorm (every wave recomputes h2 from
-//     the 2048 inputs; block 0 stores `after` and h2), then a GEMV over the
-//     fused rows [router (E) | shared_gate (1) | shared gate_proj (512) |
-//     shared up_proj (512)] -> bf16.
-//  2. moe_expert_up_kernel: grid (9 slots, 32 tiles of 16 rows): each
-//     workgroup selects the top-8 experts from the E logits itself (one wave,
-//     packed 32-bit keys reduced with DPP and permlane swaps; ties to the
-//     lower index), slot k < 8 computes 16 act rows of expert k
-//     (gate and up rows together), slot 8 the shared activation; workgroup
-//     (0, 0) stores the ids and routing weights.
+//     residual add + RMSNorm (every wave recomputes h2 from the 2048
+//     inputs; block 0 stores `after` and h2), then a GEMV over the rows
+//     [router (E) | shared_gate (1)] -> bf16.
+//  2. moe_expert_up_kernel: grid (9 slots, 32 tiles of 16 rows): slot k < 8
+//     selects the top-8 experts from the E logits itself (one wave, packed
+//     32-bit keys reduced with DPP and permlane swaps; ties to the lower
+//     index) and computes 16 act rows of expert k (gate and up rows
+//     together); slot 8 computes the shared expert's act rows from the
+//     shared gate_proj | up_proj rows of w_in, without waiting for a top-8;
+//     workgroup (0, 0) stores the ids and routing weights.
 //  3. moe_down_kernel: each wave owns 2 output rows and reads those rows of
 //     the 8 selected down matrices and the shared one, then combines.
 #include "moe_common.h"
@@ -42,8 +42,8 @@ constexpr size_t kWsH2 = kWsAfter + kMoeHidden * 2;               // bf16 [2048]
 constexpr size_t kWsIds = kWsH2 + kMoeHidden * 2;                 // int [8]
 constexpr size_t kWsRw = kWsIds + kMoeTopK * 4;                   // float [8] (bf16 values)
 constexpr size_t kWsAct = kWsRw + kMoeTopK * 4;                   // bf16 [9][512]
-constexpr size_t kWsProj = kWsAct + (kMoeTopK + 1) * kMoeInter * 2;   // bf16 [E + 1 + 1024]
-constexpr size_t kWsBytes = kWsProj + (kMoeMaxExperts + 1 + 2 * kMoeInter) * 2;
+constexpr size_t kWsProj = kWsAct + (kMoeTopK + 1) * kMoeInter * 2;   // bf16 [E + 1]: logits, shared gate
+constexpr size_t kWsBytes = kWsProj + (kMoeMaxExperts + 1) * 2;
 
 // Router GEMV rows per wave (launch 1 runs one row group per wave).
 constexpr int kRouterRows = 2;
@@ -141,37 +141,36 @@ __global__ __launch_bounds__(256, 2) void moe_router_kernel(
 // grid = (9, 32); block = 256: wave w computes act rows tile*16 + 4w .. +4 of
 // slot blockIdx.x (its 4 gate rows and 4 up rows, 8 rows x 4 KiB in flight).
 __global__ __launch_bounds__(256, 2) void moe_expert_up_kernel(
-    const bf16* __restrict__ gate_up, unsigned n_experts, char* __restrict__ ws) {
+    const bf16* __restrict__ gate_up, const bf16* __restrict__ w_in, unsigned n_experts,
+    char* __restrict__ ws) {
   const int slot = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j0 = blockIdx.y * 16 + 4 * wave;
   const bf16* proj = reinterpret_cast<const bf16*>(ws + kWsProj);
   bf16* act = reinterpret_cast<bf16*>(ws + kWsAct);
-  if (slot == kMoeTopK) {   // shared expert activation from launch 1
-    if (lane < 4) {
-      const int j = j0 + lane;
-      const float g = bf2f(proj[n_experts + 1 + j]);
-      const float u = bf2f(proj[n_experts + 1 + kMoeInter + j]);
-      act[kMoeTopK * kMoeInter + j] = f2bf(silu_f(g) * u);
-    }
-    return;
-  }
-  int ids[kMoeTopK];
-  float vals[kMoeTopK];
-  select_top8(proj, n_experts, ids, vals);
-  if (blockIdx.y == 0 && slot == 0 && wave == 0 && lane == 0) {
-    float rw[kMoeTopK];
-    routing_weights(vals, rw);
+  const bf16* wexp;
+  if (slot == kMoeTopK) {
+    // shared expert: its gate_proj | up_proj rows follow the router and
+    // shared_gate rows of w_in, in an expert's gate_up layout
+    wexp = w_in + (size_t)(n_experts + 1) * kMoeHidden;
+  } else {
+    int ids[kMoeTopK];
+    float vals[kMoeTopK];
+    select_top8(proj, n_experts, ids, vals);
+    if (blockIdx.y == 0 && slot == 0 && wave == 0 && lane == 0) {
+      float rw[kMoeTopK];
+      routing_weights(vals, rw);
 #pragma unroll
-    for (int k = 0; k < kMoeTopK; ++k) {
-      reinterpret_cast<int*>(ws + kWsIds)[k] = ids[k];
-      reinterpret_cast<float*>(ws + kWsRw)[k] = rw[k];
+      for (int k = 0; k < kMoeTopK; ++k) {
+        reinterpret_cast<int*>(ws + kWsIds)[k] = ids[k];
+        reinterpret_cast<float*>(ws + kWsRw)[k] = rw[k];
+      }
     }
-  }
-  int e = ids[0];
+    int e = ids[0];
 #pragma unroll
-  for (int k = 1; k < kMoeTopK; ++k) e = slot == k ? ids[k] : e;
-  const bf16* wexp = gate_up + (size_t)e * (2 * kMoeInter) * kMoeHidden;
+    for (int k = 1; k < kMoeTopK; ++k) e = slot == k ? ids[k] : e;
+    wexp = gate_up + (size_t)e * (2 * kMoeInter) * kMoeHidden;
+  }
   float xv[4][8];
   const bf16* h2 = reinterpret_cast<const bf16*>(ws + kWsH2);
 #pragma unroll
@@ -297,14 +296,15 @@ Q36_EXPORT int qwen36_moe_decode(const void* inp, const void* attn_out,
     if ((reinterpret_cast<uintptr_t>(p) % 16) != 0) return Q36_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  const unsigned n_in = n_experts + 1 + 2 * kMoeInter;
+  const unsigned n_in = n_experts + 1;   // router + shared_gate rows
   const unsigned groups = (n_in + kRouterRows - 1) / kRouterRows;
   hipLaunchKernelGGL(moe_router_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
                      static_cast<const bf16*>(inp), static_cast<const bf16*>(attn_out),
                      static_cast<const bf16*>(post_norm_w), static_cast<const bf16*>(w_in),
                      n_in, ws);
   hipLaunchKernelGGL(moe_expert_up_kernel, dim3(kMoeTopK + 1, kMoeInter / 16), dim3(256), 0,
-                     st, static_cast<const bf16*>(expert_gate_up), n_experts, ws);
+                     st, static_cast<const bf16*>(expert_gate_up),
+                     static_cast<const bf16*>(w_in), n_experts, ws);
   hipLaunchKernelGGL(moe_down_kernel, dim3(kMoeHidden / 8), dim3(256), 0, st,
                      static_cast<const bf16*>(expert_down), static_cast<const bf16*>(shared_down),
                      n_experts, ws, static_cast<bf16*>(out));
