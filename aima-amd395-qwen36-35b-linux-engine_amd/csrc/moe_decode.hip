@@ -217,18 +217,20 @@ __global__ __launch_bounds__(256, 2) void moe_down_kernel(
   const bf16* act = reinterpret_cast<const bf16*>(ws + kWsAct);
   const bf16* proj = reinterpret_cast<const bf16*>(ws + kWsProj);
   const bf16* after = reinterpret_cast<const bf16*>(ws + kWsAfter);
-  const bf16* dsrc[kMoeTopK + 1];
-#pragma unroll
-  for (int k = 0; k < kMoeTopK; ++k)
-    dsrc[k] = down + (size_t)ids[k] * kMoeHidden * kMoeInter;
-  dsrc[kMoeTopK] = shared_down;
   u32x4 wr[2][kMoeTopK + 1];
+  // the shared rows do not depend on the routing: request them first
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    wr[r][kMoeTopK] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+        shared_down + (size_t)(r0 + r) * kMoeInter + 8 * lane));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int r = 0; r < 2; ++r)
 #pragma unroll
-    for (int k = 0; k <= kMoeTopK; ++k)
+    for (int k = 0; k < kMoeTopK; ++k)
       wr[r][k] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-          dsrc[k] + (size_t)(r0 + r) * kMoeInter + 8 * lane));
+          down + (size_t)ids[k] * kMoeHidden * kMoeInter + (size_t)(r0 + r) * kMoeInter +
+          8 * lane));
   __builtin_amdgcn_sched_barrier(0);   // keep every weight load in flight before the FMAs
   float xa[kMoeTopK + 1][8];
 #pragma unroll
