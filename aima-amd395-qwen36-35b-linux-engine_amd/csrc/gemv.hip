@@ -9,9 +9,9 @@
 // weights, e.g. the fused [q_proj | k_proj | v_proj] rows), x [K] bf16, y [N]
 // bf16 = RNE(fp32 sum); accumulation in fp32.
 //
-// HBM-bound: 2 N K bytes of W per call.  A wave owns 4 rows at a time (2
-// for K = 4096, so the 2048-row output projections still spread over 256
-// workgroups: measured 3% faster over the 80 decode GEMVs) and
+// HBM-bound: 2 N K bytes of W per call.  A wave owns 2 rows at a time (4
+// rows per wave measured 3-5% slower over the 80 decode GEMVs: the
+// 2048-row output projections then fill only 128 workgroups) and
 // streams them with 16-byte nontemporal loads (lane l reads columns
 // 8l + 512j .. +8, so one load instruction covers 1 KiB of a row); x is
 // loaded once per wave into registers in the matching column order.  Each row
@@ -22,8 +22,7 @@
 namespace q36 {
 namespace {
 
-// rows per wave in flight: 4 rows of K = 2048, 2 of K = 4096
-template <int K> constexpr int gv_rows() { return K == 2048 ? 4 : 2; }
+constexpr int kGvRows = 2;        // rows per wave in flight
 constexpr int kGvWaves = 4;       // waves per workgroup
 
 template <int K>
@@ -31,7 +30,6 @@ __global__ __launch_bounds__(64 * kGvWaves) void gemv_bf16_kernel(
     const bf16* __restrict__ w, const bf16* __restrict__ x, bf16* __restrict__ y,
     unsigned n_rows) {
   constexpr int kSteps = K / 512;   // 1 KiB load instructions per row
-  constexpr int kGvRows = gv_rows<K>();
   const int lane = threadIdx.x & 63;
   const unsigned wave_g = blockIdx.x * kGvWaves + (threadIdx.x >> 6);
   const unsigned waves = gridDim.x * kGvWaves;
@@ -91,8 +89,7 @@ Q36_EXPORT int qwen36_gemv_bf16(const void* w, unsigned n_rows, unsigned k,
       (k != 2048u && k != 4096u) || (reinterpret_cast<uintptr_t>(w) % 16) != 0 ||
       (reinterpret_cast<uintptr_t>(x) % 16) != 0)
     return Q36_EINVAL;
-  const unsigned rows = k == 2048u ? gv_rows<2048>() : gv_rows<4096>();
-  const unsigned groups = (n_rows + rows - 1) / rows;                 // row groups
+  const unsigned groups = (n_rows + kGvRows - 1) / kGvRows;          // row groups
   unsigned blocks = (groups + kGvWaves - 1) / kGvWaves;
   if (blocks > 2048u) blocks = 2048u;                                  // grid-stride beyond
   hipStream_t st = static_cast<hipStream_t>(stream);
