@@ -18,7 +18,7 @@
 // with every bf16 rounding of the eager PyTorch text.
 //
 // Launches (all HBM-bound GEMV shapes, 16-byte nontemporal weight loads):
-//  1. moe_router_kernel: each wave first requests its 2 weight rows, then
+//  1. moe_router_kernel: each wave first requests its weight row, then
 //     residual add + RMSNorm (every wave recomputes h2 from the 2048
 //     inputs; block 0 stores `after` and h2), then a GEMV over the rows
 //     [router (E) | shared_gate (1)] -> bf16.
@@ -45,8 +45,9 @@ constexpr size_t kWsAct = kWsRw + kMoeTopK * 4;                   // bf16 [9][51
 constexpr size_t kWsProj = kWsAct + (kMoeTopK + 1) * kMoeInter * 2;   // bf16 [E + 1]: logits, shared gate
 constexpr size_t kWsBytes = kWsProj + (kMoeMaxExperts + 1) * 2;
 
-// Router GEMV rows per wave (launch 1 runs one row group per wave).
-constexpr int kRouterRows = 2;
+// Router GEMV rows per wave (launch 1 runs one row group per wave; 1 row:
+// 65 workgroups for 257 rows, measured 2% faster per token than 2 rows).
+constexpr int kRouterRows = 1;
 // Expert act rows per wave (launch 2; each needs a gate and an up row).
 constexpr int kUpRows = 2;
 // Down-projection output rows per wave (launch 3).
