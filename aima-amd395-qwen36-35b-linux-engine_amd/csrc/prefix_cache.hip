@@ -63,9 +63,19 @@ __global__ __launch_bounds__(kCopyThreads) void prefix_copy_kernel(
   const unsigned long long c1 = min(c0 + kCopyChunk, bytes);
   const char* src = to_snapshot ? live : snapshot + slot;
   char* dst = to_snapshot ? snapshot + slot : live;
-  for (unsigned long long i = c0 + 16ull * threadIdx.x; i < c1; i += 16ull * kCopyThreads) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + i));
-    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(dst + i));
+  // 4 16-byte loads per thread in flight before their stores (measured 4.5%
+  // faster than 1, and faster than 2, 8 or 16)
+  constexpr unsigned long long kStep = 16ull * kCopyThreads;
+  for (unsigned long long i = c0 + 16ull * threadIdx.x; i < c1; i += 4 * kStep) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * kStep < c1)
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + i + u * kStep));
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (i + u * kStep < c1)
+        __builtin_nontemporal_store(v[u], reinterpret_cast<u32x4*>(dst + i + u * kStep));
   }
 }
 
