@@ -29,6 +29,8 @@
 //    ticket counters (atomic latency and contention exceed the tail saved).
 #include "common.h"
 
+#include <mutex>
+
 namespace q36 {
 namespace {
 
@@ -446,14 +448,18 @@ unsigned choose_split_tokens(unsigned cache_end) {
   return per;
 }
 
+size_t workspace_bytes(unsigned nsplit) {
+  return (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_init_mutex;
+bool g_dec_freq_ready[kMaxDevices] = {};
+
 }  // namespace
 }  // namespace q36
 
 using namespace q36;
-
-size_t workspace_bytes(unsigned nsplit) {
-  return (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
-}
 
 Q36_EXPORT size_t qwen36_decode_gqa_workspace_bytes(unsigned cache_end,
                                                     unsigned split_tokens) {
@@ -489,11 +495,12 @@ static int launch_decode(bool fuse, const void* q, const void* k_new,
   return static_cast<int>(hipGetLastError());
 }
 
-static bool g_dec_freq_ready[64] = {};
-
+// One-time per-device set-up under g_init_mutex (callers may make their first
+// calls from several host threads at once).
 static int ensure_dec_inv_freq() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return Q36_EINVAL;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Q36_EINVAL;
+  std::lock_guard<std::mutex> lock(g_init_mutex);
   if (g_dec_freq_ready[dev]) return Q36_OK;
   float h[kRotaryPairs];
   rope_inv_freq_host(h);
@@ -555,3 +562,4 @@ Q36_EXPORT int qwen36_decode_step(const void* q_gate, const void* k_raw,
                        cache_end, capacity, static_cast<const bf16*>(q_gate) + kD, 2 * kD,
                        out, workspace, workspace_bytes_given, split_tokens, stream);
 }
+

@@ -9,7 +9,8 @@
 //   conv:   y = SiLU(conv4([state | x])) per channel, rounded to bf16
 //           (fle:5368-5386), new conv state = last three inputs;
 //   gating: g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b)
-//           (fle:6507-6511);
+//           rounded to bf16 (b is bf16 and torch evaluates the sigmoid in
+//           its dtype, fle:6507-6511);
 //   delta:  q, k <- l2norm; q *= 1/sqrt(128); S <- S e^g; kv = S^T k;
 //           delta = (v - kv) beta; S <- S + k (x) delta; o = S^T q
 //           (fle:5242-5276), o rounded to bf16;
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
       const float xs = ds_add(av, dtb);
       const float sp = xs > 20.0f ? xs : log1pf(expf(xs));
       gb[par][0] = ds_mul(-A, sp);
-      gb[par][1] = 1.0f / (1.0f + expf(-bv));
+      gb[par][1] = bf2f(f2bf(1.0f / (1.0f + expf(-bv))));   // sigmoid of bf16 b, in bf16
     }
     __syncthreads();
     const float* qv = ych[par];

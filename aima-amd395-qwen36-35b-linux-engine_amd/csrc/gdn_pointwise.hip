@@ -72,7 +72,7 @@ __global__ void gdn_gating_kernel(const bf16* __restrict__ a,
                                   const float* __restrict__ a_log,
                                   const float* __restrict__ dt_bias,
                                   float* __restrict__ g, float* __restrict__ beta,
-                                  unsigned tokens) {
+                                  unsigned tokens, bool beta_fp32) {
   const unsigned i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= tokens * kGdnHv) return;
   const unsigned t = i / kGdnHv, h = i % kGdnHv;
@@ -81,7 +81,8 @@ __global__ void gdn_gating_kernel(const bf16* __restrict__ a,
   const float xs = add_rn(av, dt_bias[h]);
   const float sp = xs > 20.0f ? xs : log1pf(expf(xs));
   g[i] = mul_rn(-expf(a_log[h]), sp);
-  beta[i] = 1.0f / (1.0f + expf(-bv));
+  const float sb = 1.0f / (1.0f + expf(-bv));
+  beta[i] = beta_fp32 ? sb : bf2f(f2bf(sb));
 }
 
 // grid = T*32/4 blocks of 4 waves; one wave per (token, v-head); lane holds
@@ -140,10 +141,10 @@ Q36_EXPORT int qwen36_gdn_conv1d(const void* x, unsigned x_row_stride,
 Q36_EXPORT int qwen36_gdn_gating(const void* a, const void* b,
                                  unsigned ab_row_stride, const void* a_log,
                                  const void* dt_bias, void* g, void* beta,
-                                 unsigned tokens, void* stream) {
+                                 unsigned tokens, unsigned flags, void* stream) {
   if (a == nullptr || b == nullptr || a_log == nullptr || dt_bias == nullptr ||
       g == nullptr || beta == nullptr || tokens == 0 || tokens > kMaxTokens ||
-      ab_row_stride < (unsigned)kGdnHv)
+      ab_row_stride < (unsigned)kGdnHv || (flags & ~1u) != 0)
     return Q36_EINVAL;
   const unsigned n = tokens * kGdnHv;
   hipLaunchKernelGGL(gdn_gating_kernel, dim3((n + 255) / 256), dim3(256), 0,
@@ -151,7 +152,8 @@ Q36_EXPORT int qwen36_gdn_gating(const void* a, const void* b,
                      static_cast<const bf16*>(a), static_cast<const bf16*>(b),
                      ab_row_stride, static_cast<const float*>(a_log),
                      static_cast<const float*>(dt_bias),
-                     static_cast<float*>(g), static_cast<float*>(beta), tokens);
+                     static_cast<float*>(g), static_cast<float*>(beta), tokens,
+                     (flags & 1u) != 0);
   return static_cast<int>(hipGetLastError());
 }
 

@@ -43,12 +43,14 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_output_gate": (_i32, [_vp, _i32, _vp, _u32, _vp, _u32, _vp]),
     # Gated DeltaNet
     "qwen36_gdn_conv1d": (_i32, [_vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
-    "qwen36_gdn_gating": (_i32, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp]),
+    "qwen36_gdn_gating": (_i32, [_vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _u32, _vp]),
     "qwen36_gdn_recurrent": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
                                     _vp, _vp, _vp, _u32, _vp]),
     "qwen36_gdn_chunk_prefill_workspace_bytes": (_sz, [_u32]),
     "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
                                         _vp, _vp, _vp, _u32, _vp, _sz, _vp]),
+    "qwen36_gdn_fused_gating_update": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32,
+                                              _vp, _u32, _vp, _vp, _vp, _u32, _f32, _u32, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     # decode projections
     "qwen36_gemv_bf16": (_i32, [_vp, _u32, _u32, _vp, _vp, _vp]),

@@ -46,9 +46,11 @@ def causal_conv1d(mixed_qkv: torch.Tensor, conv_state: torch.Tensor, weight: tor
 
 
 def gating(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
-           dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+           dt_bias: torch.Tensor, beta_fp32: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """g = -exp(A_log) * softplus(a + dt_bias), beta = sigmoid(b); fp32 [T, 32]
-    (fle:6507-6511)."""
+    (fle:6507-6511).  The layer's torch text evaluates sigmoid on the bf16
+    projection output, so beta is rounded to bf16 unless ``beta_fp32`` (the
+    vLLM fused gating keeps it in fp32)."""
     t = a.shape[0]
     for name, x in (("a", a), ("b", b)):
         require(x, name, torch.bfloat16, contiguous=False)
@@ -61,7 +63,7 @@ def gating(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
     g = torch.empty(t, HV, dtype=torch.float32, device=a.device)
     beta = torch.empty_like(g)
     _lib.call("qwen36_gdn_gating", ptr(a), ptr(b), a.stride(0), ptr(a_log), ptr(dt_bias),
-              ptr(g), ptr(beta), t, stream_handle(a.device))
+              ptr(g), ptr(beta), t, 1 if beta_fp32 else 0, stream_handle(a.device))
     return g, beta
 
 
@@ -281,3 +283,54 @@ class LinearAttentionLayer:
             self.ssm_state.copy_(new_state)   # keep the state buffer (prefix-cache slices)
         gated = gated_rmsnorm(core, z, w["norm"])
         return gated @ w["out_proj"].t()
+
+
+def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: float = 1.0,
+                                           threshold: float = 20.0, scale: float | None = None,
+                                           initial_state: torch.Tensor | None = None,
+                                           inplace_final_state: bool = True,
+                                           cu_seqlens=None, ssm_state_indices=None,
+                                           num_accepted_tokens=None,
+                                           use_qk_l2norm_in_kernel: bool = False):
+    """Drop-in for vLLM's ``fused_sigmoid_gating_delta_rule_update`` as the
+    reference's decode calls it (four_layer_mini_engine.py:6429-6440): one
+    sequence, gating fused into the recurrent update, state in vLLM's
+    [Hv, dv, dk] orientation (``qwen36_gdn_fused_gating_update``).
+
+    q, k [1, T, 16 (or 32), 128] bf16; v [1, T, 32, 128] bf16; a, b [T, 32]
+    (or [1, T, 32]) bf16; A_log, dt_bias [32]; initial_state [1, 32, 128, 128]
+    fp32.  Returns (o [1, T, 32, 128] bf16, final_state [1, 32, 128, 128]
+    fp32): the updated ``initial_state`` itself when ``inplace_final_state``,
+    else a new tensor.  Only the single-sequence form is provided: the
+    batching arguments (cu_seqlens, ssm_state_indices, num_accepted_tokens)
+    must be None, and beta/threshold keep vLLM's defaults (1.0, 20.0)."""
+    if cu_seqlens is not None or ssm_state_indices is not None or num_accepted_tokens is not None:
+        raise NotImplementedError("only the single-sequence form is provided")
+    if beta != 1.0 or threshold != 20.0:
+        raise NotImplementedError("softplus beta/threshold other than 1.0/20.0")
+    if initial_state is None:
+        raise ValueError("initial_state is required")
+    qv, kv_, vv, t, hq = _qkv_views(q, k, v)
+    if qv.stride(0) % 8 or vv.stride(0) != HV * DV:
+        raise ValueError("q/k token stride must be a multiple of 8; v must be contiguous")
+    a2 = a.reshape(t, HV) if a.dim() == 3 else a
+    b2 = b.reshape(t, HV) if b.dim() == 3 else b
+    for name, x in (("a", a2), ("b", b2)):
+        require(x, name, torch.bfloat16, contiguous=False)
+        if x.shape != (t, HV) or x.stride(1) != 1:
+            raise ValueError(f"{name} must be [T, 32]")
+    if a2.stride(0) != b2.stride(0):
+        raise ValueError("a and b must share a row stride")
+    s_in = initial_state.reshape(HV, DV, DK)
+    require(s_in, "initial_state", torch.float32)
+    final = s_in if inplace_final_state else torch.empty_like(s_in)
+    out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=qv.device)
+    a_log = A_log.float().contiguous()
+    dtb = dt_bias.float().contiguous()
+    if scale is None:
+        scale = DK ** -0.5
+    _lib.call("qwen36_gdn_fused_gating_update", ptr(a_log), ptr(a2), ptr(b2), a2.stride(0),
+              ptr(dtb), ptr(qv), ptr(kv_), hq, qv.stride(0), ptr(vv), vv.stride(0), ptr(s_in),
+              ptr(final), ptr(out), t, float(scale), 1 if use_qk_l2norm_in_kernel else 0,
+              stream_handle(qv.device))
+    return out, (initial_state if inplace_final_state else final.view(1, HV, DV, DK))

@@ -133,7 +133,10 @@ int qwen36_output_gate(const void* attn, int attn_is_f32, const void* q_gate,
  *   out [T,8192] = SiLU(conv).
  * qwen36_gdn_gating: the beta/g half of _fused_post_conv_kernel
  *   (four_layer_mini_engine.py:6507-6511): a, b [T, >=32 stride] bf16,
- *   A_log, dt_bias [32] fp32 -> g, beta [T,32] fp32.
+ *   A_log, dt_bias [32] fp32 -> g, beta [T,32] fp32.  flags 0: beta =
+ *   sigmoid(b) rounded to bf16, as the torch layer evaluates it on the bf16
+ *   projection output; QWEN36_GDN_BETA_FP32 (1): unrounded fp32 sigmoid, as
+ *   vLLM's fused gating.  Other flag bits are rejected.
  * qwen36_gdn_recurrent: replaces torch_recurrent_gated_delta_rule
  *   (:5242-5276) / fused_sigmoid_gating_delta_rule_update's delta rule
  *   (native_linear_layer.hip.cpp:84-95).  q,k [T, qk_heads(16|32), 128]
@@ -153,9 +156,10 @@ int qwen36_output_gate(const void* attn, int attn_is_f32, const void* q_gate,
 int qwen36_gdn_conv1d(const void* x, unsigned x_row_stride, const void* weight,
                       const void* state_in, void* state_out, void* out,
                       unsigned tokens, void* stream);
+#define QWEN36_GDN_BETA_FP32 1u
 int qwen36_gdn_gating(const void* a, const void* b, unsigned ab_row_stride,
                       const void* a_log, const void* dt_bias, void* g,
-                      void* beta, unsigned tokens, void* stream);
+                      void* beta, unsigned tokens, unsigned flags, void* stream);
 int qwen36_gdn_recurrent(const void* q, const void* k, const void* v,
                          unsigned qk_heads, unsigned qk_token_stride,
                          unsigned v_token_stride, const void* g,
@@ -173,6 +177,26 @@ int qwen36_gdn_chunk_prefill(const void* q, const void* k, const void* v,
 int qwen36_gdn_gated_norm(const void* core, const void* z,
                           unsigned z_row_stride, const void* weight, void* out,
                           unsigned tokens, void* stream);
+
+/* qwen36_gdn_fused_gating_update: the decode update in vLLM's orientation
+ *   with the gating fused -- replaces fused_sigmoid_gating_delta_rule_update
+ *   as the reference's decode calls it (four_layer_mini_engine.py:6429-6440;
+ *   native launch native_linear_layer.hip.cpp:84-95).  Per token: g =
+ *   -exp(A_log) softplus(a + dt_bias) (linear above 20), beta = sigmoid(b)
+ *   in fp32, q/k l2-normalised when flags bit 0 (use_qk_l2norm_in_kernel) is
+ *   set, q *= scale (> 0), H <- H e^g, v' = (v - H k) beta, H <- H + v' k^T,
+ *   o = H q.  A_log, dt_bias [32] fp32; a, b [T, >=32 stride] bf16; q, k
+ *   [T, qk_heads (16|32), 128] bf16 (token stride a multiple of 8, 16-byte
+ *   aligned); v [T, 32, 128] bf16 with token stride v_token_stride;
+ *   state_in -> state_out [32, 128 (v), 128 (k)] fp32, 16-byte aligned (may
+ *   alias); out [T, 32, 128] bf16. */
+int qwen36_gdn_fused_gating_update(const void* a_log, const void* a, const void* b,
+                                   unsigned ab_row_stride, const void* dt_bias,
+                                   const void* q, const void* k, unsigned qk_heads,
+                                   unsigned qk_token_stride, const void* v,
+                                   unsigned v_token_stride, const void* state_in,
+                                   void* state_out, void* out, unsigned tokens,
+                                   float scale, unsigned flags, void* stream);
 
 /* qwen36_gdn_decode_step: one launch for everything between the GDN input
  *   projections and out_proj -- conv1d + SiLU, gating, l2norm, the recurrent

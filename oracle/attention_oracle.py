@@ -206,9 +206,11 @@ def l2norm(x: torch.Tensor) -> torch.Tensor:
 
 def gdn_gating(a: torch.Tensor, b: torch.Tensor, a_log: torch.Tensor,
                dt_bias: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """fle:6507-6511 -- beta = sigmoid(b); g = -exp(A_log) * softplus(a + dt_bias),
-    both fp32 [T, Hv]."""
-    beta = torch.sigmoid(b.float())
+    """fle:6507-6511 -- beta = sigmoid(b) evaluated in b's dtype (bf16 for the
+    layer's projection output, so beta is rounded to bf16 before the delta
+    rule upcasts it); g = -exp(A_log) * softplus(a + dt_bias) in fp32.
+    Returns (g, beta), both fp32 [T, Hv]."""
+    beta = torch.sigmoid(b).float()
     g = -a_log.float().exp().unsqueeze(0) * F.softplus(a.float() + dt_bias.float().unsqueeze(0))
     return g, beta
 
@@ -305,6 +307,50 @@ def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state):
         state = state + k_t.unsqueeze(-1) * delta.unsqueeze(-2)
         out[:, :, t] = (state * q_t.unsqueeze(-1)).sum(dim=-2)
     return out.transpose(1, 2).contiguous().to(DTYPE), state
+
+
+def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, initial_state,
+                                           use_qk_l2norm_in_kernel: bool = True,
+                                           scale: float | None = None,
+                                           softplus_threshold: float = 20.0):
+    """The decode update the reference calls at fle:6429-6440 (vLLM
+    ``fused_sigmoid_gating_delta_rule_update``, vLLM
+    0.19.1rc1.dev300+g29e5d1020, module
+    ``vllm.model_executor.layers.mamba.gdn_linear_attn``; third-party code not
+    under the reference tree).  Its published algorithm, per token and value
+    head j (key head j // (Hv / Hk)):
+      g = -exp(A_log) * softplus(a + dt_bias)   (fp32, linear above 20)
+      beta = sigmoid(b)                          (fp32, not rounded)
+      q, k <- x / sqrt(sum(x^2) + 1e-6) if use_qk_l2norm_in_kernel; q *= scale
+      H <- H e^g;  v' = (v - H k) beta;  H <- H + v' (x) k;  o = H q
+    with the state H stored [Hv, dv, dk] (the transpose of the torch rule's
+    [Hv, dk, dv], fle:5433).  q, k [1, T, Hk, dk], v [1, T, Hv, dv], a, b
+    [T, Hv], initial_state [1, Hv, dv, dk] fp32 -> (o [1, T, Hv, dv] in q's
+    dtype, final_state [1, Hv, dv, dk] fp32)."""
+    hv, hk = v.shape[2], q.shape[2]
+    dk = q.shape[-1]
+    if scale is None:
+        scale = dk ** -0.5
+    x = a.float().reshape(-1, hv) + dt_bias.float().unsqueeze(0)
+    sp = torch.where(x > softplus_threshold, x, torch.log1p(torch.exp(x)))
+    g = -A_log.float().exp().unsqueeze(0) * sp
+    beta = torch.sigmoid(b.float().reshape(-1, hv))
+    qf = q[0].float().repeat_interleave(hv // hk, dim=1)
+    kf = k[0].float().repeat_interleave(hv // hk, dim=1)
+    if use_qk_l2norm_in_kernel:
+        qf = qf * torch.rsqrt(qf.pow(2).sum(-1, keepdim=True) + 1e-6)
+        kf = kf * torch.rsqrt(kf.pow(2).sum(-1, keepdim=True) + 1e-6)
+    qf = qf * scale
+    vf = v[0].float()
+    state = initial_state[0].float().clone()          # [Hv, dv, dk]
+    out = torch.empty(vf.shape, dtype=torch.float32)
+    for t in range(vf.shape[0]):
+        state = state * g[t].exp()[:, None, None]
+        pred = (state * kf[t][:, None, :]).sum(-1)     # H k   [Hv, dv]
+        vn = (vf[t] - pred) * beta[t][:, None]
+        state = state + vn[:, :, None] * kf[t][:, None, :]
+        out[t] = (state * qf[t][:, None, :]).sum(-1)   # H q
+    return out.unsqueeze(0).to(q.dtype), state.unsqueeze(0)
 
 
 def gated_rmsnorm(core: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:

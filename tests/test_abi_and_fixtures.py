@@ -67,6 +67,11 @@ def test_bad_arguments_rejected_without_launch(lib):
     # workspace too small
     assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 4096, 4096, None, 0, 1, 1, 16, 0, None) == 1
     assert L.qwen36_decode_gqa_workspace_bytes(0, 0) == 0
+    # vLLM-orientation fused gating update: bad qk_heads, flags, scale
+    fgu = L.qwen36_gdn_fused_gating_update
+    assert fgu(16, 16, 16, 32, 16, 16, 16, 8, 2048, 16, 4096, 16, 16, 16, 1, 0.088, 1, None) == 1
+    assert fgu(16, 16, 16, 32, 16, 16, 16, 16, 2048, 16, 4096, 16, 16, 16, 1, 0.088, 2, None) == 1
+    assert fgu(16, 16, 16, 32, 16, 16, 16, 16, 2048, 16, 4096, 16, 16, 16, 1, 0.0, 1, None) == 1
     assert L.qwen36_decode_gqa_workspace_bytes(131072, 0) > 0
     assert L.qwen36_gdn_recurrent(1, 1, 1, 8, 2048, 4096, 1, 1, 1, 1, 1, 1, None) == 1  # qk_heads
     assert L.qwen36_gdn_chunk_prefill(1, 1, 1, 16, 2048, 4096, 1, 1, None, 1, 1, 64, 1, 0, None) == 1
@@ -75,7 +80,8 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qwen36_output_gate(1, 0, 1, 100, 1, 1, None) == 1
     assert L.qwen36_rotary_table(None, None, 1, 0, None) == 1
     assert L.qwen36_gdn_gated_norm(1, 1, 100, 1, 1, 1, None) == 1
-    assert L.qwen36_gdn_gating(1, 1, 8, 1, 1, 1, 1, 1, None) == 1
+    assert L.qwen36_gdn_gating(1, 1, 8, 1, 1, 1, 1, 1, 0, None) == 1
+    assert L.qwen36_gdn_gating(1, 1, 32, 1, 1, 1, 1, 1, 2, None) == 1
     # fused GDN decode step: aliased / overlapping conv state, bad strides, T = 0
     good = dict(x=16, xs=8192, w=32, ci=4096, co=1 << 20, a=48, b=64, abs_=32, al=80, dt=96,
                 z=128, zs=4096, nw=160, si=256, so=256, out=512)

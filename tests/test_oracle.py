@@ -17,7 +17,18 @@ Which check pins which function:
                                recurrent; beta=0 pure decay; one step from
                                zero state; state carry across calls
   gated_rmsnorm             -> fp64 formula; weight without +1
-  full_attention layer      -> prefill(T) + decode == prefill(T+1) tail
+  full_attention layer      -> fp64 per-head brute force of the whole layer
+                               (prefill, prefix extension, decode), with
+                               mutated brute forces that must fail;
+                               prefill(T) + decode == prefill(T+1) tail
+  split_q_gate / split_gdn_qkv / repeat_kv_heads / write_kv_cache
+                            -> arange index identities, sentinel rows
+  linear_attention layer    -> fp64 per-head brute force (conv with state,
+                               key head j // 2, token-by-token delta rule,
+                               gated norm without +1), mutated variants fail
+  fused_sigmoid_gating_delta_rule_update (vLLM API)
+                            -> fp64 brute-force recurrence with fp32 beta on
+                               the transposed [Hv, dv, dk] state
 """
 import math
 
@@ -183,7 +194,15 @@ def test_l2norm_and_gating():
     g, beta = O.gdn_gating(a, b, a_log, dt)
     ref_g = -torch.exp(a_log.double()) * torch.log1p(torch.exp(a.double() + dt.double()))
     assert torch.allclose(g.double(), ref_g, rtol=1e-5)
-    assert torch.allclose(beta.double(), torch.sigmoid(b.double()), rtol=1e-6)
+    # b is bf16 (a projection output), so sigmoid(b) is evaluated and rounded
+    # in bf16 before the delta rule upcasts it (fle:6507): within half a bf16
+    # ulp of the exact sigmoid, and exactly representable in bf16
+    exact = torch.sigmoid(b.double())
+    assert ((beta.double() - exact).abs() <= 2 ** -8 * exact + 1e-12).all()
+    assert torch.equal(beta, beta.to(torch.bfloat16).float())
+    # fp32 inputs keep an fp32 sigmoid
+    _, beta32 = O.gdn_gating(a, b.float(), a_log, dt)
+    assert torch.allclose(beta32.double(), exact, rtol=1e-6)
 
 
 def brute_delta_rule(q, k, v, g, beta, s0):
@@ -338,3 +357,255 @@ def test_moe_block_forced_ids_equal_topk():
     h2 = O.layer_rmsnorm(inp + attn, w["post_attention_layernorm"])
     ids = torch.topk((h2 @ w["router"].t()).float(), 8, dim=-1).indices
     assert torch.equal(O.moe_block(inp, attn, w), O.moe_block(inp, attn, w, forced_ids=ids))
+
+
+# ---------------------------------------------------------------------------
+# Layout identities of the splitting / head-mapping / cache-write helpers
+# ---------------------------------------------------------------------------
+
+def test_split_gdn_qkv_and_repeat_layout():
+    """fle:6497-6505: columns [0,2048) are q (16 heads x 128), [2048,4096) k,
+    [4096,8192) v (32 heads x 128); value head j reads key head j // 2."""
+    x = torch.arange(2 * 8192, dtype=torch.float64).view(2, 8192)
+    q, k, v = O.split_gdn_qkv(x)
+    assert q.shape == (2, 16, 128) and k.shape == (2, 16, 128) and v.shape == (2, 32, 128)
+    t, h, d = torch.meshgrid(torch.arange(2), torch.arange(16), torch.arange(128), indexing="ij")
+    assert torch.equal(q, (t * 8192 + h * 128 + d).double())
+    assert torch.equal(k, (t * 8192 + 2048 + h * 128 + d).double())
+    t, j, d = torch.meshgrid(torch.arange(2), torch.arange(32), torch.arange(128), indexing="ij")
+    assert torch.equal(v, (t * 8192 + 4096 + j * 128 + d).double())
+    r = O.repeat_kv_heads(q)
+    assert r.shape == (2, 32, 128)
+    for jj in range(32):
+        assert torch.equal(r[:, jj], q[:, jj // 2])
+    # interleave, not tile: heads 1 and 16 read different key heads
+    assert not torch.equal(r[:, 1], q[:, 1]) and torch.equal(r[:, 1], q[:, 0])
+
+
+def test_write_kv_cache_rows():
+    """fle:5980-5986 (sequence-major): rows [start, start+T) take the new K/V,
+    every other row keeps its old contents."""
+    kc = torch.full((12, 2, 256), -7.0, dtype=torch.bfloat16)
+    vc = torch.full((12, 2, 256), -9.0, dtype=torch.bfloat16)
+    k = torch.arange(3 * 512, dtype=torch.float32).view(3, 2, 256).to(torch.bfloat16)
+    v = (-torch.arange(3 * 512, dtype=torch.float32)).view(3, 2, 256).to(torch.bfloat16)
+    O.write_kv_cache(kc, vc, k, v, 5)
+    assert torch.equal(kc[5:8], k) and torch.equal(vc[5:8], v)
+    assert (kc[:5] == -7).all() and (kc[8:] == -7).all()
+    assert (vc[:5] == -9).all() and (vc[8:] == -9).all()
+
+
+# ---------------------------------------------------------------------------
+# Whole-layer brute forces (fp64, explicit per-head / per-token loops)
+# ---------------------------------------------------------------------------
+
+def _bf(x):
+    """Round an fp64 tensor through bf16 (the reference's activation dtype)."""
+    return x.to(torch.bfloat16).double()
+
+
+def brute_full_attention(inp, w, k_cache, v_cache, start, decode, mutate=None):
+    """fp64 gated GQA layer from the definitions (fle:6546-6653), one query
+    row at a time.  Per head h the fused q-projection row holds [query(256) |
+    gate(256)] at columns 512h..; head h reads KV head h // 8; head norm is
+    x / sqrt(mean(x^2) + 1e-6) * (1 + w); RoPE rotates pairs (i, i + 32),
+    i < 32, by angle pos * 1e7^(-2i/64) at the absolute position; softmax of
+    q.k / 16 over keys 0..pos; output * sigmoid(gate); o_proj.  bf16 rounding
+    is applied where the reference holds bf16 tensors.  The K/V rows are
+    written into the (fp64) caches.  ``mutate`` names one deliberate wiring
+    error (used to show the comparison detects it)."""
+    t = inp.shape[0]
+    x = inp.double()
+    qg = _bf(x @ w["q_proj"].double().t())
+    kk = _bf(x @ w["k_proj"].double().t()).view(t, 2, 256)
+    vv = _bf(x @ w["v_proj"].double().t()).view(t, 2, 256)
+    inv = torch.tensor([1e7 ** (-2.0 * i / 64) for i in range(32)], dtype=torch.float64)
+
+    def norm_rope(vec, weight, pos):
+        y = _bf(vec / torch.sqrt(vec.pow(2).mean() + 1e-6) * (1 + weight.double()))
+        ang = pos * inv
+        c, s = torch.cos(ang), torch.sin(ang)
+        out = y.clone()
+        if mutate == "rope_interleaved":      # pairs (2i, 2i+1) instead of (i, i+32)
+            out[0:64:2] = y[0:64:2] * c - y[1:64:2] * s
+            out[1:64:2] = y[1:64:2] * c + y[0:64:2] * s
+        else:
+            out[:32] = y[:32] * c - y[32:64] * s
+            out[32:64] = y[32:64] * c + y[:32] * s
+        return _bf(out)
+
+    out = torch.zeros(t, 2048, dtype=torch.float64)
+    for i in range(t):
+        pos = start + i
+        for kv in range(2):
+            k_cache[pos, kv] = norm_rope(kk[i, kv], w["k_norm"], pos)
+            v_cache[pos, kv] = vv[i, kv]
+    for i in range(t):
+        pos = start + i
+        attn = torch.zeros(4096, dtype=torch.float64)
+        for h in range(16):
+            base = 512 * h if mutate != "gate_split" else 256 * h
+            qpos = i if mutate == "q_pos_relative" else pos   # query rotated at its chunk offset
+            qh = norm_rope(qg[i, base:base + 256], w["q_norm"], qpos)
+            gate = qg[i, base + 256:base + 512]
+            kv = h // 8 if mutate != "kv_head" else h % 2
+            keys = k_cache[:pos + 1, kv]
+            sc = keys @ qh / 16.0
+            p = torch.softmax(sc, 0)
+            o = p @ v_cache[:pos + 1, kv]
+            attn[256 * h:256 * h + 256] = _bf(o) * _bf(torch.sigmoid(gate))
+        out[i] = _bf(attn) @ w["o_proj"].double().t()
+    return out
+
+
+def test_full_attention_matches_fp64_brute_force():
+    """Pins oracle.full_attention: prefill from position 0, prefill that
+    extends the cached prefix (bottom-right mask), and a decode step, each
+    against the fp64 brute force; mutated brute forces (wrong KV head, wrong
+    gate split, RoPE pairs interleaved, queries rotated at chunk-relative
+    positions) must miss by far more than the tolerance."""
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(41)
+    w = syn.full_attention_weights(g)
+    x = syn.randn((11, 2048), g, 0.5)
+    cap = 12
+    kc = torch.zeros(cap, 2, 256, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    bk = torch.zeros(cap, 2, 256, dtype=torch.float64)
+    bv = torch.zeros_like(bk)
+    steps = [(0, 6, "prefill"), (6, 4, "prefill"), (10, 1, "decode")]
+    for start, t, mode in steps:
+        snap = (bk.clone(), bv.clone())
+        got = O.full_attention(x[start:start + t], w, kc, vc, start, mode).double()
+        ref = brute_full_attention(x[start:start + t], w, bk, bv, start, mode == "decode")
+        err = (got - ref).abs().max().item()
+        scale = ref.abs().max().item()
+        assert err <= 1e-2 * scale, (mode, start, err, scale)
+        assert torch.equal(kc[:start + t].double(), bk[:start + t])
+        assert torch.equal(vc[:start + t].double(), bv[:start + t])
+        # (a RoPE position shifted equally for queries and keys cancels in
+        # q.k, so the position mutation rotates only the queries, relative to
+        # the chunk start: it shows only when the prefill extends a prefix)
+        muts = ["kv_head", "gate_split", "rope_interleaved"] + (["q_pos_relative"] if start else [])
+        for m in muts:
+            mk, mv = snap[0].clone(), snap[1].clone()
+            bad = brute_full_attention(x[start:start + t], w, mk, mv, start, mode == "decode", m)
+            assert (got - bad).abs().max().item() >= 10 * max(err, 1e-3 * scale), (m, mode)
+
+
+def brute_linear_attention(inp, w, conv_state, ssm_state, mutate=None):
+    """fp64 Gated-DeltaNet layer from the definitions (fle:6378-6544):
+    in_proj qkv / z / a / b; per channel a causal 4-tap conv over the three
+    carried inputs then the token, SiLU; value head j uses q, k of key head
+    j // 2 (columns 128*(j//2) and 2048 + 128*(j//2)) and v columns
+    4096 + 128 j; beta = sigmoid(b) (bf16), g = -exp(A_log) softplus(a +
+    dt_bias); q, k l2-normalised, q / sqrt(128); per token S <- S e^g,
+    S <- S + k (x) beta (v - S^T k), o = S^T q; gated norm
+    o / sqrt(mean(o^2) + 1e-6) * w (no +1) * SiLU(z); out_proj.  Returns
+    (out, new_conv_state, new_ssm_state)."""
+    t = inp.shape[0]
+    x = inp.double()
+    mixed = _bf(x @ w["in_proj_qkv"].double().t())
+    z = _bf(x @ w["in_proj_z"].double().t())
+    a = _bf(x @ w["in_proj_a"].double().t())
+    b = _bf(x @ w["in_proj_b"].double().t())
+    if mutate == "swap_ab":
+        a, b = b, a
+    cw = w["conv1d"].double()
+    window = torch.cat((conv_state.double(), mixed.t()), 1)     # [8192, 3 + T]
+    y = torch.zeros(t, 8192, dtype=torch.float64)
+    for i in range(t):
+        acc = (window[:, i:i + 4] * cw).sum(1)
+        y[i] = _bf(torch.nn.functional.silu(_bf(acc)))
+    new_conv = window[:, -3:].clone()
+    s = ssm_state.double().clone()
+    core = torch.zeros(t, 32, 128, dtype=torch.float64)
+    for i in range(t):
+        for j in range(32):
+            kh = j // 2 if mutate != "tile_heads" else j % 16
+            qo, ko = (128 * kh, 2048 + 128 * kh) if mutate != "swap_qk" else (2048 + 128 * kh, 128 * kh)
+            q = y[i, qo:qo + 128]
+            k = y[i, ko:ko + 128]
+            v = y[i, 4096 + 128 * j:4096 + 128 * j + 128]
+            q = q / torch.sqrt((q * q).sum() + 1e-6) / math.sqrt(128)
+            k = k / torch.sqrt((k * k).sum() + 1e-6)
+            beta = _bf(torch.sigmoid(b[i, j]))
+            xs = a[i, j] + w["dt_bias"][j].double()
+            gg = -torch.exp(w["A_log"][j].double()) * torch.nn.functional.softplus(xs)
+            s[j] = s[j] * torch.exp(gg)
+            s[j] = s[j] + torch.outer(k, beta * (v - s[j].t() @ k))
+            core[i, j] = _bf(s[j].t() @ q)
+    gated = torch.zeros(t, 4096, dtype=torch.float64)
+    for i in range(t):
+        for j in range(32):
+            o = core[i, j]
+            nv = _bf(o / torch.sqrt(o.pow(2).mean() + 1e-6) * w["norm"].double())
+            gated[i, 128 * j:128 * j + 128] = _bf(nv * torch.nn.functional.silu(z[i, 128 * j:128 * j + 128]))
+    return gated @ w["out_proj"].double().t(), new_conv, s
+
+
+def test_linear_attention_matches_fp64_brute_force():
+    """Pins oracle.linear_attention: a chunked prefill from the zero state,
+    then two decode steps carrying conv and recurrent state, against the fp64
+    brute force (outputs within 2% of their scale, states to 1e-3 relative);
+    mutated brute forces (heads tiled instead of interleaved, q/k column
+    ranges swapped, a/b swapped) must miss by far more."""
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(42)
+    w = syn.linear_attention_weights(g, a_max=1.0)
+    w["dt_bias"] = torch.randn(32, generator=g) * 0.5
+    x = syn.randn((7, 2048), g, 0.5)
+    conv = torch.zeros(8192, 3, dtype=torch.bfloat16)
+    ssm = torch.zeros(32, 128, 128)
+    bconv = torch.zeros(8192, 3, dtype=torch.float64)
+    bssm = torch.zeros(32, 128, 128, dtype=torch.float64)
+    for lo, hi, mode in [(0, 5, "prefill"), (5, 6, "decode"), (6, 7, "decode")]:
+        snap = (bconv.clone(), bssm.clone())
+        got, conv, ssm = O.linear_attention(x[lo:hi], w, conv, ssm, mode)
+        ref, bconv, bssm = brute_linear_attention(x[lo:hi], w, bconv, bssm)
+        err = (got.double() - ref).abs().max().item()
+        scale = ref.abs().max().item()
+        assert err <= 2e-2 * scale, (mode, err, scale)
+        # the carried conv state is the last three bf16 projection rows: equal
+        # up to the last-bit rounding of fp32- vs fp64-accumulated products
+        assert ((conv.double() - bconv).abs() <= 2 ** -7 * bconv.abs()).all()
+        assert ((ssm.double() - bssm).norm() / bssm.norm()).item() <= 1e-3
+        for m in ("tile_heads", "swap_qk", "swap_ab"):
+            bad, _, _ = brute_linear_attention(x[lo:hi], w, snap[0], snap[1], m)
+            assert (got.double() - bad).abs().max().item() >= 5 * max(err, 1e-3 * scale), (m, mode)
+
+
+def test_vllm_gating_update_matches_fp64_brute_force():
+    """Pins oracle.fused_sigmoid_gating_delta_rule_update (the vLLM decode
+    API the reference calls at fle:6429-6440): fp64 brute force with fp32
+    beta = sigmoid(b) and the [Hv, dv, dk] state, 3 tokens; and with
+    use_qk_l2norm_in_kernel=False the raw q, k enter unnormalised."""
+    g = gen(43)
+    t = 3
+    q = torch.randn(1, t, 16, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, t, 16, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, t, 32, 128, generator=g).to(torch.bfloat16)
+    a = torch.randn(t, 32, generator=g).to(torch.bfloat16)
+    b = torch.randn(t, 32, generator=g).to(torch.bfloat16)
+    a_log = torch.log(torch.rand(32, generator=g) * 4 + 0.1)
+    dt = torch.randn(32, generator=g)
+    h0 = torch.randn(1, 32, 128, 128, generator=g) * 0.1
+    for norm in (True, False):
+        o, h = O.fused_sigmoid_gating_delta_rule_update(a_log, a, b, dt, q, k, v, h0, norm)
+        hh = h0[0].double().clone()
+        for i in range(t):
+            for j in range(32):
+                qq, kk = q[0, i, j // 2].double(), k[0, i, j // 2].double()
+                if norm:
+                    qq = qq / torch.sqrt((qq * qq).sum() + 1e-6)
+                    kk = kk / torch.sqrt((kk * kk).sum() + 1e-6)
+                qq = qq / math.sqrt(128)
+                xs = a[i, j].double() + dt[j].double()
+                gg = -math.exp(a_log[j].item()) * (xs.item() if xs > 20 else math.log1p(math.exp(xs.item())))
+                beta = 1 / (1 + math.exp(-b[i, j].item()))
+                hh[j] = hh[j] * math.exp(gg)
+                vn = (v[0, i, j].double() - hh[j] @ kk) * beta
+                hh[j] = hh[j] + torch.outer(vn, kk)
+                ref_o = hh[j] @ qq
+                assert (o[0, i, j].double() - ref_o).abs().max() <= 1e-2 * max(1.0, ref_o.abs().max())
+        assert ((h[0].double() - hh).norm() / hh.norm()).item() <= 1e-5
