@@ -452,8 +452,17 @@ size_t workspace_bytes(unsigned nsplit) {
   return (size_t)nsplit * kHkv * kGroup * (kD + 2) * sizeof(float);
 }
 
+// Library-owned split-partial buffer of qwen36_decode_gqa_noalloc: the
+// workspace of the largest split count (256), one copy per GPU, held until
+// the process ends.  Host code never passes `scratch` itself to a kernel
+// (its host-side name is not a device address): the device address is
+// taken once per device with hipGetSymbolAddress and kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = (size_t)kMaxSplits * kHkv * kGroup * (kD + 2) * sizeof(float);
+__device__ __align__(256) char scratch[kScratchBytes];
+
 constexpr int kMaxDevices = 64;
 std::mutex g_init_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
 bool g_dec_freq_ready[kMaxDevices] = {};
 
 }  // namespace
@@ -510,6 +519,23 @@ static int ensure_dec_inv_freq() {
   return Q36_OK;
 }
 
+// Device address of this device's `scratch` (taken on the first call on
+// each device, with that device current).
+static int scratch_ptr(void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return Q36_EINVAL;
+  std::lock_guard<std::mutex> lock(g_init_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return Q36_EINVAL;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return Q36_OK;
+}
+
 Q36_EXPORT int qwen36_decode_gqa(const void* q, const void* k_new,
                                  const void* v_new, void* k_cache,
                                  void* v_cache, unsigned position,
@@ -563,3 +589,26 @@ Q36_EXPORT int qwen36_decode_step(const void* q_gate, const void* k_raw,
                        out, workspace, workspace_bytes_given, split_tokens, stream);
 }
 
+Q36_EXPORT int qwen36_decode_gqa_noalloc(const void* q, const void* k_new,
+                                         const void* v_new, void* k_cache,
+                                         void* v_cache, unsigned position,
+                                         unsigned cache_end, unsigned capacity,
+                                         const void* gate, unsigned gate_head_stride,
+                                         void* out, unsigned split_tokens,
+                                         void* stream) {
+  if (q == nullptr || k_cache == nullptr || v_cache == nullptr ||
+      out == nullptr || cache_end == 0 || cache_end > capacity || capacity > kMaxTokens ||
+      ((k_new == nullptr) != (v_new == nullptr)) ||
+      (k_new != nullptr && position >= cache_end) ||
+      (split_tokens % (kDecWaves * kDecBlock)) != 0)
+    return Q36_EINVAL;
+  const unsigned per = split_tokens ? split_tokens : choose_split_tokens(cache_end);
+  const unsigned nsplit = (cache_end + per - 1) / per;
+  if (nsplit > kMaxSplits || workspace_bytes(nsplit) > kScratchBytes) return Q36_EINVAL;
+  void* ws = nullptr;
+  const int st = scratch_ptr(&ws);
+  if (st != Q36_OK) return st;
+  return launch_decode(false, q, k_new, v_new, FuseArgs{}, k_cache, v_cache, position,
+                       cache_end, capacity, gate, gate_head_stride, out, ws, kScratchBytes,
+                       split_tokens, stream);
+}

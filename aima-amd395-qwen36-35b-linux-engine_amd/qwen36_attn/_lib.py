@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_decode_gqa_workspace_bytes": (_sz, [_u32, _u32]),
     "qwen36_decode_gqa": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                  _vp, _u32, _vp, _vp, _sz, _u32, _vp]),
+    "qwen36_decode_gqa_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                         _vp, _u32, _vp, _u32, _vp]),
     "qwen36_decode_step": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
                                   _vp, _vp, _sz, _u32, _vp]),
     # pointwise (full attention)

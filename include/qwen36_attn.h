@@ -80,6 +80,22 @@ int qwen36_decode_gqa(const void* q, const void* k_new, const void* v_new,
                       size_t workspace_bytes, unsigned split_tokens,
                       void* stream);
 
+/* qwen36_decode_gqa_noalloc: qwen36_decode_gqa without a workspace argument.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The split partials go to a library-owned device buffer of
+ * 4,227,072 bytes (the workspace of 256 splits, the most any call uses),
+ * one per GPU, held until the process ends; the call allocates nothing.
+ * Arguments and results are those of qwen36_decode_gqa; a split count whose
+ * workspace would exceed the buffer returns 1.  Every call on one GPU shares
+ * that GPU's buffer: calls that overlap on one GPU (different streams, or
+ * concurrently replayed graphs) race. */
+int qwen36_decode_gqa_noalloc(const void* q, const void* k_new, const void* v_new,
+                              void* k_cache, void* v_cache, unsigned position,
+                              unsigned cache_end, unsigned capacity,
+                              const void* gate, unsigned gate_head_stride,
+                              void* out, unsigned split_tokens, void* stream);
+
 /* qwen36_decode_step: the whole one-token decode of a gated full-attention
  * layer between its projections and o_proj, in one split launch plus the
  * combine: head RMSNorm (w + 1) and partial RoPE of the 16 query heads and of

@@ -67,6 +67,11 @@ def test_bad_arguments_rejected_without_launch(lib):
     # workspace too small
     assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 4096, 4096, None, 0, 1, 1, 16, 0, None) == 1
     assert L.qwen36_decode_gqa_workspace_bytes(0, 0) == 0
+    # no-allocation decode: same checks, and more than 256 splits (a workspace
+    # beyond its library-owned buffer) rejected before any HIP call
+    assert L.qwen36_decode_gqa_noalloc(None, None, None, None, None, 0, 1, 1, None, 0, None, 0, None) == 1
+    assert L.qwen36_decode_gqa_noalloc(1, None, None, 1, 1, 0, 257 * 128, 257 * 128, None, 0, 1, 128,
+                                       None) == 1
     # vLLM-orientation fused gating update: bad qk_heads, flags, scale
     fgu = L.qwen36_gdn_fused_gating_update
     assert fgu(16, 16, 16, 32, 16, 16, 16, 8, 2048, 16, 4096, 16, 16, 16, 1, 0.088, 1, None) == 1
