@@ -346,66 +346,103 @@ __global__ __launch_bounds__(512) void fmha_split_combine_kernel(
   dst[1] = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
 }
 
-// Provider-owned split-K scratch (qrt_ck_fmha_prepare allocates it on the
-// current device; kept until the process ends): room for kSplitItems
-// (tile, chunk, head) partials of 256 rows.  Launches without it, or whose
-// split would not fit, run unsplit.  Launches that use it share it, so they
-// must be ordered (one stream, as the reference's engine launches them).
+// Split-K scratch: room for kSplitItems (tile, chunk, head) partials of 256
+// rows.  The reference's provider ABI has no workspace argument, so the
+// provider owns one scratch per device (allocated by qrt_ck_fmha_prepare,
+// kept until the process ends: graphs captured with a split launch hold its
+// address).  The first split launch on a device claims that scratch for its
+// stream; split launches on that stream are ordered by it, and launches on
+// any other stream run unsplit (same results, slower for short prompts), so
+// concurrent streams never share partials.  qwen36_fmha_prefill takes a
+// caller workspace instead and splits on any stream.
 constexpr unsigned kSplitItems = 512;
 constexpr size_t kSplitItemBytes = (size_t)256 * (kD + 2) * sizeof(float);
+constexpr size_t kSplitScratchBytes = kSplitItems * kSplitItemBytes;
+constexpr int kFmMaxDevices = 64;
 std::mutex g_fm_mutex;
-void* g_fm_scratch[64] = {};
+struct ProviderScratch {
+  void* ptr = nullptr;
+  bool claimed = false;
+  hipStream_t owner = nullptr;
+};
+ProviderScratch g_fm_scratch[kFmMaxDevices];
 
-void* split_scratch_for_current_device() {
+// The provider scratch if `stream` may use it (claiming it on first use).
+void* provider_scratch_for(hipStream_t stream) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kFmMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_fm_mutex);
-  return g_fm_scratch[dev];
+  ProviderScratch& ps = g_fm_scratch[dev];
+  if (ps.ptr == nullptr) return nullptr;
+  if (!ps.claimed) {
+    ps.claimed = true;
+    ps.owner = stream;
+  }
+  return ps.owner == stream ? ps.ptr : nullptr;
 }
 
+std::once_flag g_fm_attr_once;
+hipError_t g_fm_attr_status = hipSuccess;
+
+// Split plan for short prompts: too few 256-row tiles to fill the GPU, so
+// each tile's key range is cut into chunks (about 256 live workgroups).
+struct SplitPlan {
+  unsigned n_chunks, chunk_keys, items;
+};
+
+SplitPlan split_plan(unsigned q_tokens, unsigned kv_tokens) {
+  const unsigned tiles = (q_tokens + 255) / 256;
+  SplitPlan p{1u, kv_tokens, 0u};
+  if (tiles * kHq >= 256u) return p;
+  p.n_chunks = (256u + tiles * kHq - 1) / (tiles * kHq);
+  p.chunk_keys = (((kv_tokens + p.n_chunks - 1) / p.n_chunks) + kFmKv - 1) / kFmKv * kFmKv;
+  p.items = tiles * p.n_chunks * kHq;
+  if (p.n_chunks < 2 || p.items > kSplitItems) p = SplitPlan{1u, kv_tokens, 0u};
+  return p;
+}
+
+size_t split_workspace_bytes(const SplitPlan& p) {
+  return p.n_chunks > 1 ? (size_t)p.items * kSplitItemBytes : 0;
+}
+
+bool valid_geometry(const void* q, const void* k, const void* v, const float* out,
+                    unsigned q_tokens, unsigned kv_tokens) {
+  return q != nullptr && k != nullptr && v != nullptr && out != nullptr && q_tokens != 0u &&
+         q_tokens <= kMaxTokens && kv_tokens >= q_tokens && kv_tokens <= kMaxTokens;
+}
+
+// `scratch` null: run unsplit.
 int launch_fmha(const void* q, const void* k, const void* v, float* out,
-                unsigned q_tokens, unsigned kv_tokens, hipStream_t stream) {
-  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr ||
-      q_tokens == 0u || q_tokens > kMaxTokens || kv_tokens < q_tokens ||
-      kv_tokens > kMaxTokens)
-    return Q36_EINVAL;
-  static bool attr_set = false;
-  if (!attr_set) {
+                unsigned q_tokens, unsigned kv_tokens, void* scratch, hipStream_t stream) {
+  std::call_once(g_fm_attr_once, [] {
     for (const void* f : {reinterpret_cast<const void*>(fmha_prefill_kernel<8, false>),
                           reinterpret_cast<const void*>(fmha_prefill_kernel<4, false>),
                           reinterpret_cast<const void*>(fmha_prefill_kernel<2, false>),
                           reinterpret_cast<const void*>(fmha_prefill_kernel<8, true>)}) {
       const hipError_t e =
           hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFmLds);
-      if (e != hipSuccess) return (int)e;
+      if (e != hipSuccess) g_fm_attr_status = e;
     }
-    attr_set = true;
-  }
+  });
+  if (g_fm_attr_status != hipSuccess) return (int)g_fm_attr_status;
   auto tiles = [&](unsigned rows) { return (q_tokens + rows - 1) / rows; };
   const bf16* qb = static_cast<const bf16*>(q);
   const bf16* kb = static_cast<const bf16*>(k);
   const bf16* vb = static_cast<const bf16*>(v);
   const SplitArgs none{nullptr, nullptr, 0u, 1u};
-  // Too few 256-row tiles to fill the GPU: split each tile's key range into
-  // chunks (about 256 live workgroups) when the provider scratch is there.
-  if (tiles(256) * kHq < 256u) {
-    const unsigned n_chunks = (256u + tiles(256) * kHq - 1) / (tiles(256) * kHq);
-    const unsigned chunk_keys = (((kv_tokens + n_chunks - 1) / n_chunks) + kFmKv - 1) /
-                                kFmKv * kFmKv;
-    void* scratch = split_scratch_for_current_device();
-    if (n_chunks > 1 && scratch != nullptr && tiles(256) * n_chunks * kHq <= kSplitItems) {
-      SplitArgs sp;
-      sp.o = static_cast<float*>(scratch);
-      sp.ml = sp.o + (size_t)kSplitItems * 256 * kD;
-      sp.chunk_keys = chunk_keys;
-      sp.n_chunks = n_chunks;
-      hipLaunchKernelGGL((fmha_prefill_kernel<8, true>), dim3(tiles(256) * n_chunks * kHq),
-                         dim3(512), kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens,
-                         tiles(256), sp);
-      hipLaunchKernelGGL(fmha_split_combine_kernel, dim3(tiles(256) * kHq * 16), dim3(512), 0,
-                         stream, sp.o, sp.ml, out, q_tokens, kv_tokens, chunk_keys, n_chunks);
-      return static_cast<int>(hipGetLastError());
-    }
+  const SplitPlan plan = split_plan(q_tokens, kv_tokens);
+  if (plan.n_chunks > 1 && scratch != nullptr) {
+    SplitArgs sp;
+    sp.o = static_cast<float*>(scratch);
+    sp.ml = sp.o + (size_t)plan.items * 256 * kD;   // (O partials, then (m, l) pairs)
+    sp.chunk_keys = plan.chunk_keys;
+    sp.n_chunks = plan.n_chunks;
+    hipLaunchKernelGGL((fmha_prefill_kernel<8, true>), dim3(plan.items), dim3(512), kFmLds,
+                       stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), sp);
+    hipLaunchKernelGGL(fmha_split_combine_kernel, dim3(tiles(256) * kHq * 16), dim3(512), 0,
+                       stream, sp.o, sp.ml, out, q_tokens, kv_tokens, plan.chunk_keys,
+                       plan.n_chunks);
+    return static_cast<int>(hipGetLastError());
   }
   // Query rows per workgroup: 256 (8 waves) when that gives at least 256
   // workgroups or the rows extend a cached prefix (long rows); short square
@@ -425,6 +462,14 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
   return static_cast<int>(hipGetLastError());
 }
 
+int provider_launch(const void* q, const void* k, const void* v, float* out,
+                    unsigned q_tokens, unsigned kv_tokens, hipStream_t stream) {
+  if (!valid_geometry(q, k, v, out, q_tokens, kv_tokens)) return Q36_EINVAL;
+  void* scratch = split_plan(q_tokens, kv_tokens).n_chunks > 1 ? provider_scratch_for(stream)
+                                                                : nullptr;
+  return launch_fmha(q, k, v, out, q_tokens, kv_tokens, scratch, stream);
+}
+
 }  // namespace
 }  // namespace q36
 
@@ -439,14 +484,14 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
 Q36_EXPORT int qrt_ck_fmha_prepare(unsigned tokens) {
   if (tokens == 0u || tokens > q36::kMaxTokens) return Q36_EINVAL;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= q36::kFmMaxDevices) {
     (void)hipGetLastError();
     return Q36_OK;
   }
   std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
-  if (q36::g_fm_scratch[dev] == nullptr &&
-      hipMalloc(&q36::g_fm_scratch[dev], q36::kSplitItems * q36::kSplitItemBytes) != hipSuccess) {
-    q36::g_fm_scratch[dev] = nullptr;
+  q36::ProviderScratch& ps = q36::g_fm_scratch[dev];
+  if (ps.ptr == nullptr && hipMalloc(&ps.ptr, q36::kSplitScratchBytes) != hipSuccess) {
+    ps.ptr = nullptr;
     (void)hipGetLastError();
   }
   return Q36_OK;
@@ -455,16 +500,16 @@ Q36_EXPORT int qrt_ck_fmha_prepare(unsigned tokens) {
 Q36_EXPORT int qrt_ck_fmha_bf16_launch(const void* q, const void* k,
                                        const void* v, float* out,
                                        unsigned tokens, void* stream) {
-  return q36::launch_fmha(q, k, v, out, tokens, tokens,
-                          static_cast<hipStream_t>(stream));
+  return q36::provider_launch(q, k, v, out, tokens, tokens,
+                              static_cast<hipStream_t>(stream));
 }
 
 Q36_EXPORT int qrt_ck_fmha_bf16_launch_ex(const void* q, const void* k,
                                           const void* v, float* out,
                                           unsigned query_tokens,
                                           unsigned kv_tokens, void* stream) {
-  return q36::launch_fmha(q, k, v, out, query_tokens, kv_tokens,
-                          static_cast<hipStream_t>(stream));
+  return q36::provider_launch(q, k, v, out, query_tokens, kv_tokens,
+                              static_cast<hipStream_t>(stream));
 }
 
 Q36_EXPORT int qrt_ck_fmha_release(void) { return Q36_OK; }
@@ -475,8 +520,27 @@ Q36_EXPORT int qrt_ck_fmha_q8192_prepare(void) { return Q36_OK; }
 Q36_EXPORT int qrt_ck_fmha_q8192_bf16_launch(const void* q, const void* k,
                                              const void* v, float* out,
                                              void* stream) {
-  return q36::launch_fmha(q, k, v, out, 8192u, 8192u,
-                          static_cast<hipStream_t>(stream));
+  return q36::provider_launch(q, k, v, out, 8192u, 8192u,
+                              static_cast<hipStream_t>(stream));
 }
 
 Q36_EXPORT int qrt_ck_fmha_q8192_release(void) { return Q36_OK; }
+
+// ---- workspace form (no counterpart in the reference's provider ABI) -------
+Q36_EXPORT size_t qwen36_fmha_prefill_workspace_bytes(unsigned query_tokens,
+                                                      unsigned kv_tokens) {
+  if (query_tokens == 0u || query_tokens > q36::kMaxTokens || kv_tokens < query_tokens ||
+      kv_tokens > q36::kMaxTokens)
+    return 0;
+  return q36::split_workspace_bytes(q36::split_plan(query_tokens, kv_tokens));
+}
+
+Q36_EXPORT int qwen36_fmha_prefill(const void* q, const void* k, const void* v, float* out,
+                                   unsigned query_tokens, unsigned kv_tokens, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!q36::valid_geometry(q, k, v, out, query_tokens, kv_tokens)) return Q36_EINVAL;
+  const size_t need = q36::split_workspace_bytes(q36::split_plan(query_tokens, kv_tokens));
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return Q36_EINVAL;
+  return q36::launch_fmha(q, k, v, out, query_tokens, kv_tokens, need > 0 ? workspace : nullptr,
+                          static_cast<hipStream_t>(stream));
+}

@@ -642,14 +642,14 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   const unsigned n_chunks = (tokens + kC - 1) / kC;
   if (workspace_bytes < (size_t)n_chunks * kGdnHv * kUnitBytes) return Q36_EINVAL;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(gdn_chunk_prep_kernel),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)sizeof(PrepLds));
-    if (e != hipSuccess) return (int)e;
-    attr_set = true;
-  }
+  static std::once_flag attr_once;
+  static hipError_t attr_status = hipSuccess;
+  std::call_once(attr_once, [] {
+    attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_chunk_prep_kernel),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)sizeof(PrepLds));
+  });
+  if (attr_status != hipSuccess) return (int)attr_status;
   char* wsb = static_cast<char*>(workspace);
   const bf16* qb = static_cast<const bf16*>(q);
   const bf16* kb = static_cast<const bf16*>(k);

@@ -52,6 +52,7 @@
 #include "moe_common.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace q36 {
 namespace {
@@ -671,16 +672,17 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
       !aligned16(workspace))
     return Q36_EINVAL;
   const unsigned T = tokens, E = n_experts;
-  static bool attr_set = false;   // 80 KiB of dynamic LDS per GEMM workgroup
-  if (!attr_set) {
+  static std::once_flag attr_once;   // 80 KiB of dynamic LDS per GEMM workgroup
+  static hipError_t attr_status = hipSuccess;
+  std::call_once(attr_once, [] {
     for (const void* f : {reinterpret_cast<const void*>(moe_gemm_kernel<kRouter>),
                           reinterpret_cast<const void*>(moe_gemm_kernel<kGateUp>),
                           reinterpret_cast<const void*>(moe_gemm_kernel<kDown>)}) {
       const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds);
-      if (e != hipSuccess) return (int)e;
+      if (e != hipSuccess) attr_status = e;
     }
-    attr_set = true;
-  }
+  });
+  if (attr_status != hipSuccess) return (int)attr_status;
   const PfLayout L = pf_layout(T, E);
   char* ws = static_cast<char*>(workspace);
   int* ids = reinterpret_cast<int*>(ws + L.ids);

@@ -16,6 +16,8 @@
 // that the reference materialises is rounded separately (no contraction).
 #include "common.h"
 
+#include <mutex>
+
 namespace q36 {
 namespace {
 
@@ -89,11 +91,13 @@ __global__ void output_gate_kernel(const void* __restrict__ attn,
   out[i] = f2bf(mul_rn(bf2f(a), bf2f(sg)));
 }
 
+std::mutex g_freq_mutex;   // first calls may come from several host threads
 bool g_freq_ready[64] = {};
 
 int ensure_inv_freq() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return Q36_EINVAL;
+  std::lock_guard<std::mutex> lock(g_freq_mutex);
   if (g_freq_ready[dev]) return Q36_OK;
   float h[kRotaryPairs];
   rope_inv_freq_host(h);

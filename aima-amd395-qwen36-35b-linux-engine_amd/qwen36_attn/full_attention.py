@@ -124,8 +124,10 @@ def decode_step(q_gate: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 def fmha_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                  out: torch.Tensor | None = None) -> torch.Tensor:
-    """Causal GQA flash attention through the provider ABI
-    ``qrt_ck_fmha_bf16_launch_ex`` (qrt_ck_fmha_q8192_provider.cpp:306-316).
+    """Causal GQA flash attention, the computation of the provider ABI
+    ``qrt_ck_fmha_bf16_launch_ex`` (qrt_ck_fmha_q8192_provider.cpp:306-316),
+    through its workspace form ``qwen36_fmha_prefill`` (short prompts split
+    their key ranges into a workspace of this package's scratch).
 
     q [T,16,256] bf16; k, v [S,2,256] bf16 with S >= T (rows [0,S) of the
     cache, the last T of which are the new tokens); top-left mask when S == T,
@@ -144,24 +146,12 @@ def fmha_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if out is None:
         out = torch.empty(t, Q_DIM, dtype=torch.float32, device=q.device)
     require(out, "out", torch.float32, shape=(t, Q_DIM))
-    _prepare_provider(q.device)
-    _lib.call("qrt_ck_fmha_bf16_launch_ex", ptr(q), ptr(k), ptr(v), ptr(out), t, s,
-              stream_handle(q.device))
+    lib = _lib.load(("qwen36_fmha_prefill",))
+    nb = lib.qwen36_fmha_prefill_workspace_bytes(t, s)
+    ws = scratch("fmha_split", nb, q.device) if nb else None
+    _lib.call("qwen36_fmha_prefill", ptr(q), ptr(k), ptr(v), ptr(out), t, s, ptr(ws),
+              ws.numel() if ws is not None else 0, stream_handle(q.device))
     return out
-
-
-_PREPARED: set = set()
-
-
-def _prepare_provider(device: torch.device) -> None:
-    """qrt_ck_fmha_prepare once per device (allocates the provider's split-K
-    scratch, which short prompts use; it is kept for the process)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    if idx in _PREPARED:
-        return
-    with torch.cuda.device(idx):
-        _lib.call("qrt_ck_fmha_prepare", MAX_TOKENS)
-    _PREPARED.add(idx)
 
 
 class FmhaProvider:
@@ -191,10 +181,17 @@ class FmhaProvider:
         if out is None:
             out = torch.empty(q.shape[0], Q_DIM, dtype=torch.float32, device=q.device)
             self._outputs[key] = out
-        try:
-            return fmha_prefill(q, k, value, out=out)
-        except _lib.KernelError as exc:
-            raise RuntimeError(f"CK-FMHA launch failed: {exc}") from exc
+        t, s = q.shape[0], k.shape[0]
+        if q.shape != (t, HQ, HEAD_DIM) or k.shape != (s, HKV, HEAD_DIM) or value.shape != k.shape:
+            raise RuntimeError("CK-FMHA q must be [T,16,256] and k/value [S,2,256]")
+        if not (q.is_contiguous() and k.is_contiguous() and value.is_contiguous()):
+            raise RuntimeError("CK-FMHA q/k/v inputs must be contiguous")
+        lib = _lib.load(("qrt_ck_fmha_bf16_launch_ex",))
+        status = lib.qrt_ck_fmha_bf16_launch_ex(ptr(q), ptr(k), ptr(value), ptr(out), t, s,
+                                                stream_handle(q.device))
+        if status != 0:
+            raise RuntimeError(f"CK-FMHA launch failed: hip_status={status}")
+        return out
 
     def release(self) -> None:
         _lib.call("qrt_ck_fmha_release")

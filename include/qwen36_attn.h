@@ -37,10 +37,14 @@ extern "C" {
  * 132 MiB split-K scratch: launches with fewer than 16 query tiles of 256
  * rows split each tile's key range over several workgroups plus a combine
  * launch and use it (without it -- not prepared, or the allocation failed, in
- * which case prepare still returns 0 -- they run unsplit).  Launches that use it must
- * be ordered (one stream).  The scratch is kept until the process ends
+ * which case prepare still returns 0 -- they run unsplit).  The first split
+ * launch on a device claims the scratch for its stream: later launches on
+ * that stream are ordered by it, launches on other streams run unsplit, so
+ * launches on different streams never share it.  (Replaying a graph captured
+ * on the owning stream concurrently with that stream's own launches is the
+ * one way to race on it.)  The scratch is kept until the process ends
  * (graphs captured with a split launch hold its address), so release has
- * nothing to free. */
+ * nothing to free; the provider's globals sit behind a mutex. */
 int qrt_ck_fmha_prepare(unsigned tokens);
 int qrt_ck_fmha_bf16_launch(const void* q, const void* k, const void* v,
                             float* out, unsigned tokens, void* stream);
@@ -48,6 +52,17 @@ int qrt_ck_fmha_bf16_launch_ex(const void* q, const void* k, const void* v,
                                float* out, unsigned query_tokens,
                                unsigned kv_tokens, void* stream);
 int qrt_ck_fmha_release(void);
+/* qwen36_fmha_prefill: the same attention with a caller-owned split-K
+ * workspace (no counterpart in the reference's provider ABI), so short
+ * prompts split on any stream: workspace of at least
+ * qwen36_fmha_prefill_workspace_bytes(query_tokens, kv_tokens) bytes (0 =
+ * this geometry runs unsplit and workspace may be NULL; also 0 for invalid
+ * geometry, which the launch rejects).  Calls that overlap on one workspace
+ * race. */
+size_t qwen36_fmha_prefill_workspace_bytes(unsigned query_tokens, unsigned kv_tokens);
+int qwen36_fmha_prefill(const void* q, const void* k, const void* v, float* out,
+                        unsigned query_tokens, unsigned kv_tokens, void* workspace,
+                        size_t workspace_bytes, void* stream);
 /* Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300);
  * the fp32-packed q8192 launch is not provided. */
 int qrt_ck_fmha_q8192_prepare(void);

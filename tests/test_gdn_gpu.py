@@ -213,3 +213,36 @@ def test_chunk_prefill_graph_replays_match_eager(gpu):
         assert torch.equal(fin, ref_s), i
         G.chunk_gated_delta_rule(qd[:100], kd[:100], vd[:100], gd[:100], bd[:100], None)
         torch.cuda.synchronize()
+
+
+def test_config4_conv_from_mixed_qkv_then_chunk_prefill(gpu):
+    """Config 4 from its first step: the depthwise causal conv + SiLU over
+    mixed_qkv [8192, 8192] (zero conv state), its output split into q, k
+    [8192, 16, 128] and v [8192, 32, 128] in place, then the chunked prefill
+    (chunk 64) from the zero state -- against the oracle's conv, split,
+    head repeat and chunked rule (fle:5293-5403, 6497-6505, 5167-5240)."""
+    from qwen36_attn import gated_deltanet as G
+    t = 8192
+    g = syn.gen(44)
+    mixed = syn.randn((t, 8192), g)
+    w = syn.randn((8192, 4), g, 0.5)
+    _, _, _, gg, beta = syn.gdn_core_inputs(t, g, a_max=16.0)
+    print("gdn config4 conv + chunk prefill", flush=True)
+    zero = torch.zeros(8192, 3, dtype=torch.bfloat16)
+    conv_d, st_d = G.causal_conv1d(mixed.to(gpu), zero.to(gpu), w.to(gpu))
+    q = conv_d[:, :2048].view(t, 16, 128)
+    k = conv_d[:, 2048:4096].view(t, 16, 128)
+    v = conv_d[:, 4096:].view(t, 32, 128)
+    out, st = G.chunk_gated_delta_rule(q, k, v, gg.to(gpu), beta.to(gpu), None)
+    torch.cuda.synchronize()
+    ref_conv, ref_cst = O.causal_conv1d(mixed, zero, w)
+    assert (conv_d.cpu().float() - ref_conv.float()).abs().max().item() <= TOL_OUT
+    assert (conv_d.cpu() == ref_conv).float().mean().item() >= 0.99
+    assert torch.equal(st_d.cpu(), ref_cst)
+    rq, rk, rv = O.split_gdn_qkv(ref_conv)
+    R = O.repeat_kv_heads
+    ref_o, ref_s = O.chunk_gated_delta_rule(R(rq).unsqueeze(0), R(rk).unsqueeze(0),
+                                            rv.unsqueeze(0), gg.unsqueeze(0), beta.unsqueeze(0),
+                                            torch.zeros(1, 32, 128, 128))
+    assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
+    assert rel_err(st.cpu(), ref_s) <= TOL_STATE

@@ -159,3 +159,105 @@ def test_prefill_max_tokens_sampled_rows(gpu, t, s):
         assert (got[r:r + 1].cpu() - ref).abs().max().item() <= TOL_TIGHT, r
     del q, k, v, got
     torch.cuda.empty_cache()
+
+
+def test_short_prefills_on_two_streams(gpu):
+    """Two short prompts (split-K launches) enqueued on two streams at once,
+    through the provider ABI (the provider scratch belongs to the first
+    stream that splits; the other stream's launch runs unsplit) and through
+    qwen36_fmha_prefill with one workspace per stream: every output equals
+    the oracle."""
+    from qwen36_attn import _lib
+    lib = _lib.load()
+    assert lib.qrt_ck_fmha_prepare(1024) == 0
+    cases = [_inputs(300, 300, seed=91), _inputs(500, 1400, seed=92)]
+    refs = [O.prefill_attention(q, k, v, k.shape[0] - q.shape[0], out_dtype=torch.float32)
+            for q, k, v in cases]
+    streams = [torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)]
+    dev = [tuple(x.to(gpu) for x in c) for c in cases]
+    for form in ("provider", "workspace"):
+        print(f"two-stream short prefill ({form})", flush=True)
+        outs, keep = [], []
+        torch.cuda.synchronize()
+        for rep in range(3):
+            for (q, k, v), s in zip(dev, streams):
+                out = torch.full((q.shape[0], 4096), float("nan"), device=gpu)
+                with torch.cuda.stream(s):
+                    h = s.cuda_stream
+                    if form == "provider":
+                        rc = lib.qrt_ck_fmha_bf16_launch_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                            out.data_ptr(), q.shape[0], k.shape[0], h)
+                    else:
+                        nb = lib.qwen36_fmha_prefill_workspace_bytes(q.shape[0], k.shape[0])
+                        assert nb > 0
+                        ws = torch.empty(nb, dtype=torch.uint8, device=gpu)
+                        keep.append(ws)
+                        rc = lib.qwen36_fmha_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                                     out.data_ptr(), q.shape[0], k.shape[0],
+                                                     ws.data_ptr(), nb, h)
+                    assert rc == 0
+                outs.append(out)
+        torch.cuda.synchronize()
+        for i, out in enumerate(outs):
+            assert (out.cpu() - refs[i % 2]).abs().max().item() <= TOL_TIGHT, (form, i)
+    # the workspace form rejects a missing or short workspace for a split geometry
+    q, k, v = dev[0]
+    out = torch.empty(q.shape[0], 4096, device=gpu)
+    nb = lib.qwen36_fmha_prefill_workspace_bytes(q.shape[0], k.shape[0])
+    assert lib.qwen36_fmha_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                   q.shape[0], k.shape[0], None, 0, None) == 1
+    assert lib.qwen36_fmha_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                   q.shape[0], k.shape[0], 1, nb - 1, None) == 1
+    assert lib.qwen36_fmha_prefill_workspace_bytes(8192, 8192) == 0
+
+
+def test_config3_norm_rope_kv_write_and_gated_output(gpu):
+    """Config 3 end to end: raw Q|gate [8192, 16 x 512], K/V new [8192, 2,
+    256] and a 4096-row cached prefix.  Head norm + RoPE at absolute positions
+    4096..12287 write K (normalised) and V (raw) into cache rows 4096..12287;
+    the FMHA runs bottom-right causal over the 12288 rows; the sigmoid gate is
+    applied.  Written rows vs the oracle's head_rmsnorm / apply_rope /
+    write_kv_cache (V bit-exact, K to the bf16 bar with >= 99% bit-equal),
+    the gated output on sampled rows vs the oracle's SDPA + output_gate
+    (fle:5151-5162, 5980-5986, 6627-6650)."""
+    from qwen36_attn.full_attention import fmha_prefill, head_norm_rope_kv_write, output_gate
+    from qwen36_attn import synthetic as syn
+    t, pre = 8192, 4096
+    s = pre + t
+    g = syn.gen(33)
+    qg = syn.randn((t, 8192), g)
+    kn = syn.randn((t, 512), g)
+    vn = syn.randn((t, 512), g)
+    qw = syn.randn((256,), g, 0.1)
+    kw = syn.randn((256,), g, 0.1)
+    kc = torch.zeros(s, 2, 256, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kc[:pre] = syn.randn((pre, 2, 256), g)
+    vc[:pre] = syn.randn((pre, 2, 256), g)
+    print("config3 norm+rope+kv write + fmha + gate", flush=True)
+    kcd, vcd = kc.to(gpu), vc.to(gpu)
+    qgd = qg.to(gpu)
+    q = head_norm_rope_kv_write(qgd, kn.to(gpu), vn.to(gpu), qw.to(gpu), kw.to(gpu), kcd, vcd, pre)
+    attn32 = fmha_prefill(q, kcd, vcd)
+    gated = output_gate(attn32, qgd).cpu()
+    kcg, vcg, qh = kcd.cpu(), vcd.cpu(), q.cpu()
+    # oracle: the same three steps on the CPU
+    cos, sin = O.rope_cos_sin(pre, t)
+    q_ref, gate_ref = O.split_q_gate(qg)
+    q_ref = O.apply_rope(O.head_rmsnorm(q_ref, qw), cos, sin)
+    k_ref = O.apply_rope(O.head_rmsnorm(kn.view(t, 2, 256), kw), cos, sin)
+    O.write_kv_cache(kc, vc, k_ref, vn.view(t, 2, 256), pre)
+    assert torch.equal(vcg, vc)                      # raw V rows, and the prefix untouched
+    assert torch.equal(kcg[:pre], kc[:pre])
+    dk = (kcg[pre:].float() - kc[pre:].float()).abs()
+    assert dk.max().item() <= TOL and (dk == 0).float().mean().item() >= 0.99
+    dq = (qh.float() - q_ref.float()).abs()
+    assert dq.max().item() <= TOL and (dq == 0).float().mean().item() >= 0.99
+    # sampled rows of the gated output (rows are independent); the oracle
+    # attends with its own K rows and the kernel's Q rows
+    rows = [0, 1, 255, 256, 4095, 4096, 8191]
+    for r in rows:
+        lim = pre + r + 1
+        a = O.prefill_attention(qh[r:r + 1], kc[:lim], vc[:lim], lim - 1, out_dtype=torch.float32)
+        ref = O.output_gate(a.to(torch.bfloat16), gate_ref[r:r + 1])
+        assert (gated[r:r + 1].float() - ref.float()).abs().max().item() <= TOL, r
