@@ -56,6 +56,8 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_fused_gating_update": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32,
                                               _vp, _u32, _vp, _vp, _vp, _u32, _f32, _u32, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
+    # prefill projections
+    "qwen36_prefill_gemm_bf16": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     # decode projections
     "qwen36_gemv_bf16": (_i32, [_vp, _u32, _u32, _vp, _vp, _vp]),
     # MoE block

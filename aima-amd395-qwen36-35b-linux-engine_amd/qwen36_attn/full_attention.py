@@ -261,9 +261,10 @@ class FullAttentionLayer:
     ``full_attention(inp, layer_index, weights)``
     (four_layer_mini_engine.py:6546-6653).
 
-    Projections use torch matmul (they are outside the attention hot path);
-    head-norm + RoPE + KV write, the attention core (FMHA provider for
-    prefill, split-K decode) and the output gate run in the HIP library.
+    Everything runs in the HIP library: the projections (prefill GEMM over
+    the fused q|gate, k, v rows and o_proj; one-token GEMVs in decode),
+    head-norm + RoPE + KV write, the attention core (FMHA for prefill,
+    split-K decode) and the output gate.
     ``weights``: q_proj [8192,2048], k_proj/v_proj [512,2048],
     o_proj [2048,4096], q_norm/k_norm [256] (all bf16 on the GPU)."""
 
@@ -299,9 +300,13 @@ class FullAttentionLayer:
                                self.v_cache, position_start, cache_end)
             from .projections import gemv
             return gemv(w["o_proj"], attn)
-        q_gate = inp @ w["q_proj"].t()
-        k = inp @ w["k_proj"].t()
-        v = inp @ w["v_proj"].t()
+        from .prefill_gemm import linear
+        if self._qkv is None:
+            from .projections import FusedProjection
+            self._qkv = FusedProjection(w["q_proj"], w["k_proj"], w["v_proj"])
+        # one GEMM over the fused [q|gate; k; v] rows; the three outputs are
+        # column views of its [T, 9216] result
+        q_gate, k, v = self._qkv.split_rows(linear(inp, self._qkv.w))
         if mode == "decode":
             if t != 1:
                 raise ValueError("decode takes one token")
@@ -315,7 +320,7 @@ class FullAttentionLayer:
                                         self.k_cache, self.v_cache, position_start)
             attn32 = fmha_prefill(q, self.k_cache[:cache_end], self.v_cache[:cache_end])
             attn = output_gate(attn32, q_gate)
-        return attn @ w["o_proj"].t()
+        return linear(attn, w["o_proj"])
 
 
 def _decode_with_strided_gate(q, k_cache, v_cache, cache_end, gate_view):

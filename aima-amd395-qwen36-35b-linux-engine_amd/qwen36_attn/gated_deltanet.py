@@ -211,9 +211,9 @@ def gdn_decode_step(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
 class LinearAttentionLayer:
     """One Gated-DeltaNet layer with its carried conv and recurrent states,
     mirroring ``linear_attention(inp, layer_index, weights)``
-    (fle:6378-6544, plain-torch branch).  Projections are torch matmuls (outside
-    the hot path); conv, gating, delta rule and gated norm run in the HIP
-    library.  ``weights``: in_proj_qkv [8192,2048], in_proj_z [4096,2048],
+    (fle:6378-6544, plain-torch branch).  Everything runs in the HIP library:
+    the projections (prefill GEMM over the fused qkv|z|b|a rows and out_proj,
+    one-token GEMVs in decode), conv, gating, delta rule and gated norm.  ``weights``: in_proj_qkv [8192,2048], in_proj_z [4096,2048],
     in_proj_a/in_proj_b [32,2048], conv1d [8192,4], A_log [32], dt_bias [32],
     norm [128], out_proj [2048,4096]."""
 
@@ -256,17 +256,21 @@ class LinearAttentionLayer:
                                     w["A_log"], w["dt_bias"], z, w["norm"], self.ssm_state)
             self.conv_state, self.conv_spare = self.conv_spare, self.conv_state
             return gemv(w["out_proj"], gated)
-        mixed = inp @ w["in_proj_qkv"].t()
-        z = inp @ w["in_proj_z"].t()
-        b = inp @ w["in_proj_b"].t()
-        a = inp @ w["in_proj_a"].t()
+        from .prefill_gemm import linear
+        from .projections import FusedProjection
+        if self._in_proj is None:
+            self._in_proj = FusedProjection(w["in_proj_qkv"], w["in_proj_z"],
+                                            w["in_proj_b"], w["in_proj_a"])
+        # one GEMM over the fused [qkv; z; b; a] rows; column views of the
+        # [T, 12352] result feed the conv, gating and gated norm in place
+        mixed, z, b, a = self._in_proj.split_rows(linear(inp, self._in_proj.w))
         if mode == "decode" and fused:
             if self.conv_spare is None:
                 self.conv_spare = torch.empty_like(self.conv_state)
             gated = gdn_decode_step(mixed, self.conv_state, self.conv_spare, w["conv1d"], a, b,
                                     w["A_log"], w["dt_bias"], z, w["norm"], self.ssm_state)
             self.conv_state, self.conv_spare = self.conv_spare, self.conv_state
-            return gated @ w["out_proj"].t()
+            return linear(gated, w["out_proj"])
         conv_out, _ = causal_conv1d(mixed, self.conv_state, w["conv1d"], new_state=self.conv_state)
         t = conv_out.shape[0]
         q = conv_out[:, :KEY_DIM].view(t, HK, DK)
@@ -282,7 +286,7 @@ class LinearAttentionLayer:
                                              final_state=new_state)
             self.ssm_state.copy_(new_state)   # keep the state buffer (prefix-cache slices)
         gated = gated_rmsnorm(core, z, w["norm"])
-        return gated @ w["out_proj"].t()
+        return linear(gated, w["out_proj"])
 
 
 def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: float = 1.0,

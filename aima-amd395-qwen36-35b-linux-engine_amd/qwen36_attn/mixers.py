@@ -106,7 +106,7 @@ class MixerState:
             self.linear_attention_initial_ssm_states[i], self.linear_attention_ssm_states[i] = b, a
 
     def fused_projection(self, layer_index: int, kind: str, *weights: torch.Tensor) -> FusedProjection:
-        """Row-concatenated decode projection weights, built once per layer
+        """Row-concatenated projection weights, built once per layer
         (rebuilt if the weight tensors change)."""
         key = (layer_index, kind)
         tag = tuple((w.data_ptr(), tuple(w.shape)) for w in weights)
@@ -169,9 +169,8 @@ def full_attention(inp: torch.Tensor, layer_index: int, weights: dict) -> torch.
                               st.position_start, st.position_end)
         return gemv(w["o_proj"], attn)
     cache_end = st.position_end if st.position_start > 0 else t
-    q_gate = pg.linear(inp, w["q_proj"])
-    k = pg.linear(inp, w["k_proj"])
-    v = pg.linear(inp, w["v_proj"])
+    proj = st.fused_projection(layer_index, "qkv", w["q_proj"], w["k_proj"], w["v_proj"])
+    q_gate, k, v = proj.split_rows(pg.linear(inp, proj.w))
     q = fa.head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"], k_cache, v_cache,
                                    st.position_start)
     attn32 = fa.fmha_prefill(q, k_cache[:cache_end], v_cache[:cache_end])
@@ -204,25 +203,16 @@ def linear_attention(inp: torch.Tensor, layer_index: int, weights: dict) -> torc
     ssm_in = st.linear_attention_initial_ssm_states[layer_index]
     ssm_out = st.linear_attention_ssm_states[layer_index]
     cw = _conv_weight(w)
+    proj = st.fused_projection(layer_index, "qkvzba", w["linear_in_proj_qkv"],
+                               w["linear_in_proj_z"], w["linear_in_proj_b"],
+                               w["linear_in_proj_a"])
+    # one GEMV (one token) or GEMM over the fused [qkv; z; b; a] rows
+    mixed, z, b, a = proj(inp) if t == 1 else proj.split_rows(pg.linear(inp, proj.w))
     if st.mode == "decode":
-        if t == 1:
-            proj = st.fused_projection(layer_index, "qkvzba", w["linear_in_proj_qkv"],
-                                       w["linear_in_proj_z"], w["linear_in_proj_b"],
-                                       w["linear_in_proj_a"])
-            mixed, z, b, a = proj(inp)
-        else:
-            mixed = pg.linear(inp, w["linear_in_proj_qkv"])
-            z = pg.linear(inp, w["linear_in_proj_z"])
-            b = pg.linear(inp, w["linear_in_proj_b"])
-            a = pg.linear(inp, w["linear_in_proj_a"])
         gated = gd.gdn_decode_step(mixed, conv_in, conv_out, cw, a, b, w["linear_A_log"],
                                    w["linear_dt_bias"], z, w["linear_norm"], ssm_in,
                                    final_state=ssm_out)
         return gemv(w["linear_out_proj"], gated) if t == 1 else pg.linear(gated, w["linear_out_proj"])
-    mixed = pg.linear(inp, w["linear_in_proj_qkv"])
-    z = pg.linear(inp, w["linear_in_proj_z"])
-    b = pg.linear(inp, w["linear_in_proj_b"])
-    a = pg.linear(inp, w["linear_in_proj_a"])
     conv, _ = gd.causal_conv1d(mixed, conv_in, cw, new_state=conv_out)
     q = conv[:, :gd.KEY_DIM].view(t, gd.HK, gd.DK)
     k = conv[:, gd.KEY_DIM:2 * gd.KEY_DIM].view(t, gd.HK, gd.DK)

@@ -1,11 +1,30 @@
-"""Prefill projections: y = x W^T for T tokens (the reference's
-``inp @ weights[...].t()``, four_layer_mini_engine.py:6566-6573 and
-:6386-6395; native prefill GEMM plans native_full_prefill.hip.cpp:552-560)."""
+"""Prefill projections on the HIP MFMA GEMM (``qwen36_prefill_gemm_bf16``):
+y = x W^T for T tokens, the reference's ``inp @ weights[...].t()``
+(four_layer_mini_engine.py:6566-6573 full attention, :6386-6395 Gated
+DeltaNet), which its native prefill runs as hipBLASLt plans
+(native_full_prefill.hip.cpp:552-560)."""
 from __future__ import annotations
 
 import torch
 
+from . import _lib
+from ._tensors import ptr, require, stream_handle
 
-def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """x [T, K] bf16, w [N, K] bf16 -> [T, N] bf16 (fp32 accumulation)."""
-    return x @ w.t()
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [T, K] bf16 (unit inner stride, row stride a multiple of 8), w [N, K]
+    bf16 contiguous -> [T, N] bf16 (fp32 accumulation, one rounding)."""
+    require(x, "x", torch.bfloat16, contiguous=False)
+    require(w, "w", torch.bfloat16)
+    if x.dim() != 2 or w.dim() != 2 or x.shape[1] != w.shape[1] or x.stride(1) != 1:
+        raise ValueError("x must be [T, K] with unit inner stride and w [N, K]")
+    t, k = x.shape
+    n = w.shape[0]
+    if out is None:
+        out = torch.empty(t, n, dtype=torch.bfloat16, device=x.device)
+    require(out, "out", torch.bfloat16, contiguous=False)
+    if out.shape != (t, n) or out.stride(1) != 1:
+        raise ValueError("out must be [T, N] with unit inner stride")
+    _lib.call("qwen36_prefill_gemm_bf16", ptr(x), x.stride(0), ptr(w), ptr(out), out.stride(0),
+              t, n, k, stream_handle(x.device))
+    return out

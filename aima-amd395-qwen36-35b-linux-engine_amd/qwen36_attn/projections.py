@@ -41,3 +41,7 @@ class FusedProjection:
     def __call__(self, x: torch.Tensor) -> list[torch.Tensor]:
         y = gemv(self.w, x)
         return list(torch.split(y, self.splits, dim=1))
+
+    def split_rows(self, y: torch.Tensor) -> list[torch.Tensor]:
+        """Column views [T, N_i] of a [T, sum N_i] product with ``self.w``."""
+        return list(torch.split(y, self.splits, dim=1))

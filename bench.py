@@ -31,7 +31,6 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-FP32_PEAK_TFLOPS = 157.3
 DECODE_BYTES_PER_TOKEN = 2048          # K + V bytes per cached token per layer
 PREFILL_FLOP_PER_PAIR = 16384          # 4 * Hq * D
 N_FULL_LAYERS = 10
@@ -299,6 +298,37 @@ def bench_decode_projections(torch, dev, iters, warmup, use_graph, native=True, 
             "hbm_gbs": nbytes / (us * 1e-6) / 1e9, "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+PREFILL_PROJ_SHAPES = [(9216, 2048), (2048, 4096), (12352, 2048), (2048, 4096)]
+
+
+def bench_prefill_projections(torch, dev, t, iters, warmup, native=True, seed=13):
+    """The prefill projections of one full-attention layer (fused q|gate,k,v
+    [9216, 2048] and o_proj [2048, 4096]) and one Gated-DeltaNet layer
+    (fused qkv|z|b|a [12352, 2048] and out_proj [2048, 4096]) for a prompt
+    of t tokens: the HIP MFMA GEMM (``native``) or torch.matmul (hipBLASLt)."""
+    from qwen36_attn.prefill_gemm import linear
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    ws = [(torch.randn(n, k, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+          for n, k in PREFILL_PROJ_SHAPES]
+    xs = {k: (torch.randn(t, k, generator=gen, device=dev) * 0.5).to(torch.bfloat16)
+          for k in (2048, 4096)}
+    outs = [torch.empty(t, n, dtype=torch.bfloat16, device=dev) for n, _ in PREFILL_PROJ_SHAPES]
+
+    def step():
+        for w, o in zip(ws, outs):
+            x = xs[w.shape[1]]
+            if native:
+                linear(x, w, out=o)
+            else:
+                torch.matmul(x, w.t(), out=o)
+    ms = Timer(torch).time(step, iters, warmup)
+    flop = sum(2 * t * n * k for n, k in PREFILL_PROJ_SHAPES)
+    del ws, xs, outs
+    return {"tokens": t, "gemms": len(PREFILL_PROJ_SHAPES), "ms": ms,
+            "tflops": flop / (ms * 1e-3) / 1e12,
+            "frac_bf16_mfma": flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
 def bench_moe_decode(torch, dev, layers, iters, warmup, use_graph, seed=7):
     """One decode token through the MoE blocks of ``layers`` layers (256
     experts, top-8, intermediate 512, shared expert), distinct weights per
@@ -489,10 +519,11 @@ def bench_gdn_decode_step(torch, dev, layers, iters, warmup, use_graph, fused=Tr
 def bench_config1_layers(torch, dev, t, iters, warmup, seed=12):
     """Config 1: one gated full-attention layer and one Gated-DeltaNet layer
     (random weights of the model's shapes) prefilling T tokens from an empty
-    cache / zero state -- projections through torch (hipBLASLt), attention,
-    norms and the GDN core through this library -- and one decode step of
-    each after the prompt (the native one-token path: fused projection
-    GEMVs, fused step kernels).  Times are per layer call."""
+    cache / zero state -- every launch from this library: the prefill GEMMs
+    over the fused projection rows, norms/RoPE/KV write, FMHA, the GDN conv,
+    gating, chunked rule and gated norm -- and one decode step of each after
+    the prompt (fused projection GEMVs, fused step kernels).  Times are per
+    layer call."""
     from qwen36_attn import synthetic as syn
     from qwen36_attn.full_attention import FullAttentionLayer
     from qwen36_attn.gated_deltanet import LinearAttentionLayer
@@ -524,14 +555,27 @@ def bench_gdn_prefill(torch, dev, t, iters, warmup, seed=3):
     fs = torch.empty(32, 128, 128, dtype=torch.float32, device=dev)
     ms = Timer(torch).time(lambda: G.chunk_gated_delta_rule(q, k, v, gg, beta, None, final_state=fs),
                            iters, warmup)
-    c = 64
-    flop_per_unit = 6 * 2 * c * c * 128 + 4 * 2 * c * 128 * 128 + c ** 3 // 3
-    flop = flop_per_unit * (t // c) * 32
-    nbytes = 2 * t * 16 * 128 * 2 + t * 32 * 128 * 2 * 2 + t * 32 * 4 * 2 + 32 * 128 * 128 * 4
+    flop, nbytes = gdn_prefill_work(t)
+    # Two rooflines (the pass is neither purely MFMA- nor HBM-bound): the
+    # algorithmic FLOP against the bf16 dense MFMA peak, and the essential
+    # bytes (q, k, v, o, g, beta, state) against HBM.  The kernels issue
+    # about 3x the algorithmic products (fp32-accurate bf16 hi/lo splits),
+    # which neither fraction credits.
     return {"tokens": t, "ms": ms, "tflops": flop / (ms * 1e-3) / 1e12,
-            "frac_fp32_mfma": flop / (ms * 1e-3) / 1e12 / FP32_PEAK_TFLOPS,
             "frac_bf16_mfma": flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
-            "hbm_gbs_algorithmic": nbytes / (ms * 1e-3) / 1e9}
+            "hbm_gbs_algorithmic": nbytes / (ms * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def gdn_prefill_work(t, c=64):
+    """Algorithmic FLOP and essential HBM bytes of a chunked delta-rule
+    prefill of t tokens (32 v-heads, dk = dv = 128): per (chunk, v-head)
+    6 x 2C^2 d + 4 x 2C d^2 + C^3 / 3; bytes = q, k (16 heads) and v, o (32
+    heads) in bf16, g and beta in fp32, the fp32 state written once."""
+    flop_per_unit = 6 * 2 * c * c * 128 + 4 * 2 * c * 128 * 128 + c ** 3 // 3
+    flop = flop_per_unit * ((t + c - 1) // c) * 32
+    nbytes = 2 * t * 16 * 128 * 2 + t * 32 * 128 * 2 * 2 + t * 32 * 4 * 2 + 32 * 128 * 128 * 4
+    return flop, nbytes
 
 
 def cpu_baseline(torch, cache_end):
@@ -557,6 +601,72 @@ def cpu_baseline(torch, cache_end):
             "cores": threads, "kind": "port",
             "sample": f"median of {len(times)} single-layer grouped-bf16 decodes at "
                       f"S={cache_end} (oracle, torch CPU, {_cpu_info()}), x{N_FULL_LAYERS} layers"}
+
+
+def _median_time(fn, min_runs=3, budget_s=8.0, max_runs=20):
+    fn()  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_prefill_baseline(torch, rows=256):
+    """Config 3 on this host's cores: the oracle's SDPA (fp32 evaluation of
+    the bf16 inputs, as the FMHA provider returns fp32) for the last ``rows``
+    query rows of the 8192-token block over the 12288-row cache (the rows
+    with the most keys), scaled to the whole block by unmasked (q, k) pairs."""
+    from oracle import attention_oracle as O
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(17)
+    t_full, s_full = 8192, 12288
+    q = torch.randn(rows, 16, 256, generator=gen).to(torch.bfloat16)
+    k = torch.randn(s_full, 2, 256, generator=gen).to(torch.bfloat16)
+    v = torch.randn(s_full, 2, 256, generator=gen).to(torch.bfloat16)
+    med, n = _median_time(lambda: O.prefill_attention(q, k, v, s_full - rows, out_dtype=torch.float32))
+    scale = causal_pairs(t_full, s_full) / causal_pairs(rows, s_full)
+    ms = med * scale * 1e3
+    flop = PREFILL_FLOP_PER_PAIR * causal_pairs(t_full, s_full)
+    return {"value": ms, "unit": "ms", "tflops": flop / (ms * 1e-3) / 1e12, "cores": threads,
+            "kind": "port",
+            "sample": f"median of {n} oracle SDPA runs (torch CPU fp32, {_cpu_info()}) over the last "
+                      f"{rows} query rows x {s_full} keys, scaled x{scale:.1f} by unmasked pairs to "
+                      f"8192 rows over a 4096-token prefix"}
+
+
+def cpu_gdn_baseline(torch, chunk_tokens=512, steps=8):
+    """Config 4 on this host's cores: the oracle's chunked delta rule
+    (fp32, chunk 64, 32 v-heads) over ``chunk_tokens`` tokens scaled
+    linearly (the chunk loop is sequential and every chunk costs the same)
+    to 8192, plus ``steps`` recurrent steps scaled to 64."""
+    from oracle import attention_oracle as O
+    from qwen36_attn import synthetic as syn
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = syn.gen(19)
+    q, k, v, gg, beta = syn.gdn_core_inputs(chunk_tokens + steps, g, a_max=16.0)
+    R = O.repeat_kv_heads
+    qr, kr = R(q).unsqueeze(0), R(k).unsqueeze(0)
+    vv, gb, bb = v.unsqueeze(0), gg.unsqueeze(0), beta.unsqueeze(0)
+    s0 = torch.zeros(1, 32, 128, 128)
+    c = chunk_tokens
+    med_c, n_c = _median_time(lambda: O.chunk_gated_delta_rule(
+        qr[:, :c], kr[:, :c], vv[:, :c], gb[:, :c], bb[:, :c], s0))
+    med_r, n_r = _median_time(lambda: O.recurrent_gated_delta_rule(
+        qr[:, c:], kr[:, c:], vv[:, c:], gb[:, c:], bb[:, c:], s0))
+    prefill_ms = med_c * (8192 / c) * 1e3
+    decode_us = med_r / steps * 1e6
+    flop, _ = gdn_prefill_work(8192)
+    return {"prefill_8k_ms": prefill_ms, "prefill_tflops": flop / (prefill_ms * 1e-3) / 1e12,
+            "recurrent_us_per_step": decode_us, "cores": threads, "kind": "port",
+            "sample": f"median of {n_c} oracle chunked-rule runs over {c} tokens scaled x{8192 // c} "
+                      f"to 8192, median of {n_r} runs of {steps} recurrent steps (torch CPU fp32, "
+                      f"{_cpu_info()})"}
 
 
 def run_only(torch, fa, dev, args):
@@ -629,6 +739,12 @@ def main():
                                                              use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
         "config1_layers_1k": bench_config1_layers(torch, dev, 1024, 20, 3),
+        "prefill_projections_1k": bench_prefill_projections(torch, dev, 1024, 20, 3),
+        "prefill_projections_1k_torch": bench_prefill_projections(torch, dev, 1024, 20, 3,
+                                                                  native=False),
+        "prefill_projections_8k": bench_prefill_projections(torch, dev, 8192, 10, 2),
+        "prefill_projections_8k_torch": bench_prefill_projections(torch, dev, 8192, 10, 2,
+                                                                  native=False),
         "moe_prefill_8k": bench_moe_prefill(torch, dev, 8192, 10, 2),
         "moe_prefill_1k": bench_moe_prefill(torch, dev, 1024, 20, 3),
         "moe_prefill_8k_torch_expert_loop": bench_moe_prefill(torch, dev, 8192, 3, 1, native=False),
@@ -645,6 +761,9 @@ def main():
                 "kernel": "qwen36_decode_gqa (write_kv_row + decode_gqa_split + decode_gqa_combine)",
                 "algorithmic_bytes_per_launch": alg_bytes}
     cpu = None if args.no_cpu else cpu_baseline(torch, 131072)
+    if not args.no_cpu:
+        extra["cpu_prefill_config3"] = cpu_prefill_baseline(torch)
+        extra["cpu_gdn_config4"] = cpu_gdn_baseline(torch)
     line = {
         "metric": "decode attn us/tok + HBM GB/s @128K ctx; prefill attn TFLOP/s @8K tokens",
         "value": head["us_per_token"], "unit": "us/token", "n_gpus": 1,

@@ -251,6 +251,20 @@ int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
                            const void* state_in, void* state_out, void* out,
                            unsigned tokens, void* stream);
 
+/* ---- prefill projections ---------------------------------------------------
+ * qwen36_prefill_gemm_bf16: y[m, n] = x[m, k] W[n, k]^T for a prompt of m
+ * tokens, bf16 in and out with fp32 accumulation (one rounding); replaces
+ * the reference's prefill projection GEMMs (hipBLASLt plans,
+ * native_full_prefill.hip.cpp:552-560, native_prefill_gemm_plans.hip.cpp;
+ * torch form `inp @ W.t()` in four_layer_mini_engine.py:6566-6573, :6386-6395,
+ * :6653, :6544).  x row-major with row stride ldx (>= k, a multiple of 8), W
+ * row-major [n, k] (out x in features), y row-major with row stride ldy
+ * (>= n); x and W 16-byte aligned; k a multiple of 32 (<= 16384), n <= 65536,
+ * m <= 262144. */
+int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y,
+                             unsigned ldy, unsigned m, unsigned n, unsigned k,
+                             void* stream);
+
 /* ---- decode projections ----------------------------------------------------
  * qwen36_gemv_bf16: y[N] = W[N,K] x[K] for one token, bf16 in and out with
  * fp32 accumulation; replaces the decode projection GEMVs
