@@ -10,7 +10,8 @@
 // Layout: k_cache, v_cache are [capacity, 2, 256] bf16 (token stride 512).
 //
 // Kernel plan (HBM-bound, 2048 bytes of K+V per token):
-//  * grid = (nsplit, 2 KV heads); the cache's 32-token blocks are dealt to
+//  * grid = nsplit x 2 KV heads (head = workgroup index % 2, so each XCD
+//    serves one head); the cache's 32-token blocks are dealt to
 //    the splits round-robin (and to the 4 waves of a split in turn), so the
 //    grid sweeps the cache as one contiguous window.
 //  * per block: S^T = K Q^T on MFMA 16x16x32 (A = K streamed from HBM into
@@ -86,8 +87,13 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
     unsigned nsplit, DecodeWs ws, FuseArgs fz) {
   __shared__ __attribute__((aligned(16))) char lds[kDecLds];
-  const int kvh = blockIdx.y;
-  const unsigned split = blockIdx.x;
+  // Workgroup i streams KV head i % 2: consecutive workgroups are dealt to
+  // the 8 XCDs in turn, so each XCD serves one head (the half of every
+  // 1 KiB cache row that head owns).  Measured on MI355X against a
+  // (split, head) grid that gives every XCD both heads: 128K 496 vs 507 us,
+  // 32K 194 vs 210 us per 10 layers, same box.
+  const int kvh = blockIdx.x & 1;
+  const unsigned split = blockIdx.x >> 1;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;   // MFMA row/column index
@@ -493,7 +499,7 @@ static int launch_decode(bool fuse, const void* q, const void* k_new,
   ws.ml = ws.o + (size_t)nsplit * kHkv * kGroup * kD;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto kernel = fuse ? decode_gqa_split_kernel<true> : decode_gqa_split_kernel<false>;
-  hipLaunchKernelGGL(kernel, dim3(nsplit, kHkv), dim3(256), 0, st,
+  hipLaunchKernelGGL(kernel, dim3(nsplit * kHkv), dim3(256), 0, st,
                      static_cast<const bf16*>(q), static_cast<bf16*>(k_cache),
                      static_cast<bf16*>(v_cache), static_cast<const bf16*>(k_new),
                      static_cast<const bf16*>(v_new), position, cache_end, nsplit, ws,

@@ -18,8 +18,8 @@
 // explicit vmcnt waits keep later fetches in flight.
 //
 // Three tile shapes (256x256, 128x256, 128x128); the host picks the one
-// with the fewest tile-area x rounds of workgroups over the 256 CUs, so short
-// prompts still spread over the chip.  Work items are dealt to the 8 XCDs in
+// with the lowest tiles-per-CU x measured tile time, so short prompts still
+// spread over the chip.  Work items are dealt to the 8 XCDs in
 // contiguous ranges that sweep 8 row tiles per column tile, so the
 // workgroups of one XCD share A rows and W rows through its L2.
 #include "common.h"
@@ -228,11 +228,15 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
     }
 }
 
+// Cost of a launch = tiles per CU (workgroups / 256, rounded up) x the
+// measured time of one tile of the shape on MI355X (K = 2048): 256x256
+// 63 us, 128x256 38 us, 128x128 20.5 us (two per CU).  Fitted on
+// M = 512..8192 x N = 2048, 9216, 12352; it picks the fastest of the three
+// at each of those shapes.
 template <class C>
-long long tile_cost(unsigned M, unsigned N) {
+long long tile_cost(unsigned M, unsigned N, int tile_time) {
   const long long wgs = (long long)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
-  const long long slots = 256LL * C::MINWG;
-  return (wgs + slots - 1) / slots * (long long)C::BM * C::BN / C::MINWG;
+  return (wgs + 255) / 256 * tile_time;
 }
 
 std::once_flag g_gemm_attr_once;
@@ -286,7 +290,8 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
   a.N = n;
   a.K = k;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const long long cl = tile_cost<CfgL>(m, n), cm = tile_cost<CfgM>(m, n), cs = tile_cost<CfgS>(m, n);
+  const long long cl = tile_cost<CfgL>(m, n, 630), cm = tile_cost<CfgM>(m, n, 380),
+                  cs = tile_cost<CfgS>(m, n, 205);
   if (cl <= cm && cl <= cs) return launch_cfg<CfgL>(a, st);
   if (cm <= cs) return launch_cfg<CfgM>(a, st);
   return launch_cfg<CfgS>(a, st);

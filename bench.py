@@ -43,7 +43,8 @@ def _parse():
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
-    p.add_argument("--only", choices=["decode", "prefill", "gdn", "moe", "moe_decode", "copy"], default=None,
+    p.add_argument("--only", choices=["decode", "prefill", "prefill_8k", "prefill_c3", "gdn", "moe",
+                                      "moe_decode", "gemm", "copy"], default=None,
                    help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
 
@@ -680,6 +681,12 @@ def run_only(torch, fa, dev, args):
              bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup),
              bench_prefill(torch, fa, dev, 1024, 1024, args.steps, args.warmup),
              bench_prefill(torch, fa, dev, 1024, 5120, args.steps, args.warmup)]
+    elif args.only == "prefill_8k":
+        r = bench_prefill(torch, fa, dev, 8192, 8192, args.steps, args.warmup)
+    elif args.only == "prefill_c3":
+        r = bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup)
+    elif args.only == "gemm":
+        r = bench_prefill_projections(torch, dev, 8192, args.steps, args.warmup)
     elif args.only == "gdn":
         r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
