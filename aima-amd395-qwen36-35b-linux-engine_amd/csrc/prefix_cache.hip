@@ -187,18 +187,32 @@ Q36_EXPORT int qwen36_prefix_cache_finalize(void* pool, unsigned long long* byte
   if (p->finalized || p->slices.empty()) return Q36_EINVAL;
   hipError_t e = hipGetDevice(&p->device);   // entries live on the current device
   if (e != hipSuccess) return (int)e;
-  p->terminal_offset = p->bytes;
   const unsigned long long per_entry = p->bytes + p->terminal_bytes;
-  e = hipMalloc(reinterpret_cast<void**>(&p->table), p->slices.size() * sizeof(SliceDesc));
-  if (e != hipSuccess) return (int)e;
-  e = hipMemcpy(p->table, p->slices.data(), p->slices.size() * sizeof(SliceDesc),
+  // All-or-nothing: on any failure everything allocated here is freed and
+  // the pool is left as it was before the call, so finalize may be retried.
+  SliceDesc* table = nullptr;
+  std::vector<char*> snaps;
+  auto fail = [&](hipError_t err) {
+    for (char* q : snaps) (void)hipFree(q);
+    if (table != nullptr) (void)hipFree(table);
+    (void)hipGetLastError();
+    return (int)err;
+  };
+  e = hipMalloc(reinterpret_cast<void**>(&table), p->slices.size() * sizeof(SliceDesc));
+  if (e != hipSuccess) return fail(e);
+  e = hipMemcpy(table, p->slices.data(), p->slices.size() * sizeof(SliceDesc),
                 hipMemcpyHostToDevice);
-  if (e != hipSuccess) return (int)e;
-  p->entries.resize(p->n_entries);
-  for (Entry& en : p->entries) {
-    e = hipMalloc(reinterpret_cast<void**>(&en.snapshot), per_entry);
-    if (e != hipSuccess) return (int)e;
+  if (e != hipSuccess) return fail(e);
+  for (unsigned i = 0; i < p->n_entries; ++i) {
+    char* q = nullptr;
+    e = hipMalloc(reinterpret_cast<void**>(&q), per_entry);
+    if (e != hipSuccess) return fail(e);
+    snaps.push_back(q);
   }
+  p->terminal_offset = p->bytes;
+  p->table = table;
+  p->entries.resize(p->n_entries);
+  for (unsigned i = 0; i < p->n_entries; ++i) p->entries[i].snapshot = snaps[i];
   p->finalized = true;
   if (bytes_out) *bytes_out = per_entry * p->n_entries;
   return Q36_OK;

@@ -110,3 +110,29 @@ def test_lookup_longest_prefix_and_lru_capture_slot(gpu):
     with pytest.raises(KernelError):
         pool.restore(5)
     pool.close()
+
+
+def test_finalize_failure_leaves_pool_unfinalized_and_frees(gpu):
+    """An entry snapshot that cannot be allocated (a 1 TiB fixed slice) makes
+    finalize return the allocation error; whatever it had allocated (the
+    device slice table, earlier snapshots) is freed and the pool stays
+    unfinalized (capture / restore refuse it), so nothing leaks."""
+    import ctypes
+    from qwen36_attn import _lib
+    lib = _lib.load()
+    buf = torch.zeros(4096, dtype=torch.uint8, device=gpu)
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info(gpu)
+    pool = lib.qwen36_prefix_cache_create(1024, 4096, 2)
+    assert pool
+    assert lib.qwen36_prefix_cache_add_slice(pool, buf.data_ptr(), 1 << 40, 0) == 0
+    nbytes = ctypes.c_ulonglong(0)
+    assert lib.qwen36_prefix_cache_finalize(pool, ctypes.byref(nbytes)) != 0
+    free1, _ = torch.cuda.mem_get_info(gpu)
+    assert abs(free1 - free0) < (64 << 20)
+    toks = (ctypes.c_uint * 4)(1, 2, 3, 4)
+    idx = ctypes.c_uint(0)
+    assert lib.qwen36_prefix_cache_capture(pool, toks, 4, buf.data_ptr(), None, ctypes.byref(idx),
+                                           None) != 0
+    assert lib.qwen36_prefix_cache_restore(pool, 0, None, None) != 0
+    assert lib.qwen36_prefix_cache_destroy(pool) == 0
