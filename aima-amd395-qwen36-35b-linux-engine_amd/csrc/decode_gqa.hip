@@ -21,9 +21,9 @@
 //    ds_read_b64_tr_b16.  The P^T operand is the S^T accumulator itself
 //    (same lane mapping), so no shuffles are needed between the two MFMAs.
 //  * the 4 waves merge in LDS; the workgroup writes one (m, l, O) partial.
-//  * decode_gqa_combine merges the partials of all splits with one load
-//    round per thread, normalises, optionally applies the sigmoid output gate
-//    and writes bf16.  Tried and measured slower on MI355X: merging in the
+//  * decode_gqa_combine_wave merges the partials of all splits (one wave per
+//    query head and 16 dims, one load round, shuffle reductions), normalises,
+//    optionally applies the sigmoid output gate and writes bf16.  Tried and measured slower on MI355X: merging in the
 //    split kernel (a "last workgroup merges" tree or a grid barrier: device-
 //    scope fences write back/invalidate the whole L2, and workgroups polling
 //    a counter slow the stream), and dynamic tail balancing through global
@@ -364,77 +364,74 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
 
 }
 
-// grid = (16 heads, 16 chunks of 16 dims); block = 256.  Thread t reads the
-// (m, l) of split t and, as (split group t/4, dim quad t%4), the float4
-// partials of splits t/4 + 64u (u < 4): every load is issued up front (one
-// memory round trip).  The split weights 2^(m - M) go through LDS; the
-// weighted partials are reduced over the wave's 16 split groups with
-// shuffles and over the 4 waves through LDS.
+// Combine: one wave per (query head, 16 dims), grid = 256 single-wave
+// workgroups.  Every load (the split partials, their (m, l), the gate) is
+// issued up front: one memory round trip.
 constexpr int kCombineDims = 16;
-static_assert(kMaxSplits == 256, "one (m, l) per combine thread");
+static_assert(kMaxSplits % 16 == 0, "16 split groups per combine wave");
 
-__global__ __launch_bounds__(256) void decode_gqa_combine_kernel(
+// Lane = (split group sg = lane / 4, dim quad dq = lane % 4); split group sg
+// takes splits sg, sg + 16, ...  The max, the weights 2^(m - M) and the sums
+// reduce over the 16 split groups with xor shuffles (lane bits 2..5): no LDS,
+// no barrier.  Measured on MI355X against a 4-wave combine with LDS
+// reductions: -0.2 to -0.7 us per layer.
+__global__ __launch_bounds__(64) void decode_gqa_combine_wave_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     unsigned nsplit, const bf16* __restrict__ gate, unsigned gate_head_stride,
     bf16* __restrict__ out) {
-  __shared__ float fw[kMaxSplits];
-  __shared__ float wred[2][4];
-  __shared__ f32x4 part[4][4];
-  const int head = blockIdx.x;
+  const int head = blockIdx.x & 15;
   const int kvh = head / kGroup, hh = head % kGroup;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int dq = tid & 3, sgp = tid >> 2;
-  const int d0 = blockIdx.y * kCombineDims + 4 * dq;
-  const size_t base = (size_t)kvh * nsplit * kGroup + hh;  // slot of split 0
-
-  float2 ml = float2{-INFINITY, 0.f};
-  if ((unsigned)tid < nsplit)
-    ml = *reinterpret_cast<const float2*>(ws_ml + (base + (size_t)tid * kGroup) * 2);
-  f32x4 os[4];
+  const int lane = threadIdx.x;
+  const int dq = lane & 3, sg = lane >> 2;
+  const int d0 = (blockIdx.x >> 4) * kCombineDims + 4 * dq;
+  const size_t base = (size_t)kvh * nsplit * kGroup + hh;
+  constexpr int kPer = kMaxSplits / 16;   // at most 16 splits per group
+  float2 ml[kPer];
+  f32x4 os[kPer];
+  float gv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (gate != nullptr && sg == 0) {
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const unsigned sp = sgp + 64 * u;
-    os[u] = sp < nsplit
-                ? *reinterpret_cast<const f32x4*>(ws_o + (base + (size_t)sp * kGroup) * kD + d0)
-                : f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int e = 0; e < 4; ++e) gv[e] = bf2f(gate[(size_t)head * gate_head_stride + d0 + e]);
   }
-  float mx = wave_max_xor(ml.x, 1);
-  mx = wave_max_xor(mx, 2);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const unsigned sp = sg + 16 * u;
+    if (sp < nsplit) {
+      ml[u] = *reinterpret_cast<const float2*>(ws_ml + (base + (size_t)sp * kGroup) * 2);
+      os[u] = *reinterpret_cast<const f32x4*>(ws_o + (base + (size_t)sp * kGroup) * kD + d0);
+    } else {
+      ml[u] = float2{-INFINITY, 0.f};
+      os[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) mx = fmaxf(mx, ml[u].x);
   mx = wave_max_xor(mx, 4);
   mx = wave_max_xor(mx, 8);
   mx = wave_max_xor(mx, 16);
   mx = wave_max_xor(mx, 32);
-  if (lane == 0) wred[0][wave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(wred[0][0], wred[0][1]), fmaxf(wred[0][2], wred[0][3]));
-  const float f = ml.x == -INFINITY ? 0.f : exp2f(ml.x - M);
-  fw[tid] = f;
-  float lsum = f * ml.y;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o, 64);
-  if (lane == 0) wred[1][wave] = lsum;
-  __syncthreads();
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
 #pragma unroll
-  for (int u = 0; u < 4; ++u) acc += fw[(sgp + 64 * u) & (kMaxSplits - 1)] * os[u];
+  for (int u = 0; u < kPer; ++u) {
+    const float f = ml[u].x == -INFINITY ? 0.f : exp2f(ml[u].x - mx);
+    L += f * ml[u].y;
+    acc += f * os[u];
+  }
 #pragma unroll
-  for (int o = 4; o < 64; o <<= 1)
+  for (int o = 4; o < 64; o <<= 1) {
+    L += __shfl_xor(L, o, 64);
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[e] += __shfl_xor(acc[e], o, 64);
-  if (lane < 4) part[wave][dq] = acc;
-  __syncthreads();
-  if (tid < 4) {
-    const float L = (wred[1][0] + wred[1][1]) + (wred[1][2] + wred[1][3]);
-    const f32x4 a = (part[0][dq] + part[1][dq]) + (part[2][dq] + part[3][dq]);
+  }
+  if (sg == 0) {
     bf16x4 ob;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      bf16 x = f2bf(a[e] / L);
+      bf16 x = f2bf(acc[e] / L);
       if (gate != nullptr) {
-        // Reference gate numerics (native_pointwise.hip.cpp:207-222): sigmoid
-        // in fp32, rounded to bf16, product rounded to bf16.
-        const float gv = bf2f(gate[(size_t)head * gate_head_stride + d0 + e]);
-        const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv)));
+        const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv[e])));
         x = f2bf(bf2f(x) * bf2f(sg_b));
       }
       ob[e] = x;
@@ -504,7 +501,7 @@ static int launch_decode(bool fuse, const void* q, const void* k_new,
                      static_cast<bf16*>(v_cache), static_cast<const bf16*>(k_new),
                      static_cast<const bf16*>(v_new), position, cache_end, nsplit, ws,
                      fz);
-  hipLaunchKernelGGL(decode_gqa_combine_kernel, dim3(kHq, kD / kCombineDims), dim3(256),
+  hipLaunchKernelGGL(decode_gqa_combine_wave_kernel, dim3(kHq * (kD / kCombineDims)), dim3(64),
                      0, st, ws.o, ws.ml, nsplit, static_cast<const bf16*>(gate),
                      gate_head_stride, static_cast<bf16*>(out));
   return static_cast<int>(hipGetLastError());
