@@ -8,14 +8,16 @@
 //
 // Tiling (gfx950): a workgroup of 8 waves computes a BM x BN tile; wave
 // (wm, wn) owns RB x CB blocks of 32 x 32 on v_mfma_f32_32x32x16_bf16 (one
-// 16-byte LDS read per operand fragment).  K advances 32 per stage through
-// a 4-stage LDS ring filled straight from global memory by buffer_load ...
+// 16-byte LDS read per operand fragment).  K advances 64 per stage through
+// an LDS ring filled straight from global memory by buffer_load ...
 // lds (16 bytes per lane, 1 KiB per instruction; rows past M or N read as
 // zeros through the buffer range check).  The 16-byte chunks of a stage row
-// are XOR-swizzled by (row / 4) mod 4, which keeps the ds_read_b128 operand
-// reads free of bank conflicts.  One barrier per stage; the fetch of stage
-// s + 3 is issued once every wave has finished reading stage s - 1, and
-// explicit vmcnt waits keep later fetches in flight.
+// are XOR-swizzled by (row / rows per 256-byte window) mod chunks per row,
+// which keeps the ds_read_b128 operand reads free of bank conflicts.  One
+// barrier per stage; the refill of a stage is issued once every wave has
+// finished reading it, explicit vmcnt waits keep later fetches in flight,
+// and the operand fragments of the next 32 K are read into a second register
+// set while the current ones feed the MFMAs.
 //
 // Three tile shapes (256x256, 128x256, 128x128); the host picks the one
 // with the lowest tiles-per-CU x measured tile time, so short prompts still
@@ -48,9 +50,12 @@ struct GemmCfg {
   static_assert(BM % Rpi == 0, "A rows fill whole instructions");
   static_assert(Stages >= 2 && Stages <= 4, "ring depth");
 };
-using CfgL = GemmCfg<4, 2, 2, 4, 1, 32, 4>;   // 256 x 256, 128 KiB LDS
-using CfgM = GemmCfg<2, 2, 2, 4, 1, 32, 4>;   // 128 x 256,  96 KiB LDS
-using CfgS = GemmCfg<2, 1, 2, 4, 2, 32, 4>;   // 128 x 128,  64 KiB LDS, 2 per CU
+// K = 64 per stage, two stages: each fetch instruction reads 8 whole 128-byte
+// rows (with 32 per stage it read 16 half lines); measured on MI355X
+// 8-13% faster than 32 per stage x 4 stages at every model shape.
+using CfgL = GemmCfg<4, 2, 2, 4, 1, 64, 2>;   // 256 x 256, 128 KiB LDS
+using CfgM = GemmCfg<2, 2, 2, 4, 1, 64, 2>;   // 128 x 256,  96 KiB LDS
+using CfgS = GemmCfg<2, 1, 2, 4, 2, 64, 2>;   // 128 x 128,  64 KiB LDS, 2 per CU
 
 __device__ __forceinline__ void g_fetch(unsigned lds_addr, int voff, const u32x4& rsrc) {
   asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
@@ -144,31 +149,35 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
 #pragma unroll
     for (int j = 0; j < C::CB; ++j) acc[i][j] = f32x16{};
 
-  // Software pipeline over K steps (stage = step % 4; the fetch of step t is
-  // issued 4 steps ahead, into the stage whose fragments were just taken):
-  //   iteration s: wait for this wave's fetch of step s + 1, barrier (every
-  //   wave's fetches of s + 1 landed, every read of step s done), fetch step
-  //   s + 4 into stage s, read step s + 1's fragments into the other register
-  //   set, then the MFMAs of step s on fragments already in registers -- so
-  //   the LDS reads of the next step overlap this step's MFMAs.
+  // Software pipeline over half-steps of 32 K (a stage holds BK / 32 of
+  // them; the fetch of step t is issued Stages steps ahead, into the stage
+  // whose fragments were just taken):
+  //   half-step h: if h + 1 starts a new step t, wait for this wave's fetch
+  //   of t, barrier (every wave's fetches of t landed, every read of step
+  //   t - 1 done), fetch step t - 1 + Stages into the stage of t - 1; read
+  //   half h + 1's fragments into the other register set; then the MFMAs of
+  //   half h on fragments already in registers -- so the LDS reads of the
+  //   next half overlap this half's MFMAs.
+  constexpr int kHS = C::BK / 32;        // half-steps per stage
   const int nsteps = (int)(p.K / C::BK);
-  constexpr int kS = C::BK / 16;
-  bf16x8 fa[2][kS][C::RB], fb[2][kS][C::CB];
-  auto read_frags = [&](int step, bf16x8 (&a)[kS][C::RB], bf16x8 (&b)[kS][C::CB]) {
-    const char* st = lds + (step % C::Stages) * C::StageB;
+  const int nh = nsteps * kHS;
+  bf16x8 fa[2][2][C::RB], fb[2][2][C::CB];
+  auto read_half = [&](int h, bf16x8 (&a)[2][C::RB], bf16x8 (&b)[2][C::CB]) {
+    const char* st = lds + ((h / kHS) % C::Stages) * C::StageB;
+    const int sub0 = (h % kHS) * 2;
 #pragma unroll
-    for (int s = 0; s < kS; ++s) {
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int cb = 0; cb < C::CB; ++cb)
-        b[s][cb] = *reinterpret_cast<const bf16x8*>(st + (brow + 32 * cb) * C::RowB + koff[s]);
+        b[s][cb] = *reinterpret_cast<const bf16x8*>(st + (brow + 32 * cb) * C::RowB + koff[sub0 + s]);
 #pragma unroll
       for (int rb = 0; rb < C::RB; ++rb)
-        a[s][rb] = *reinterpret_cast<const bf16x8*>(st + (arow + 32 * rb) * C::RowB + koff[s]);
+        a[s][rb] = *reinterpret_cast<const bf16x8*>(st + (arow + 32 * rb) * C::RowB + koff[sub0 + s]);
     }
   };
-  auto mfmas = [&](const bf16x8 (&a)[kS][C::RB], const bf16x8 (&b)[kS][C::CB]) {
+  auto mfmas = [&](const bf16x8 (&a)[2][C::RB], const bf16x8 (&b)[2][C::CB]) {
 #pragma unroll
-    for (int s = 0; s < kS; ++s)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int rb = 0; rb < C::RB; ++rb)
 #pragma unroll
@@ -187,29 +196,32 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
   for (int st = 0; st < issued; ++st) fetch(st);
   wait_fetch(0, issued);
   __syncthreads();
-  read_frags(0, fa[0], fb[0]);
-  auto iteration = [&](int step, bf16x8 (&ca)[kS][C::RB], bf16x8 (&cb)[kS][C::CB],
-                       bf16x8 (&na)[kS][C::RB], bf16x8 (&nb)[kS][C::CB]) {
-    if (step + 1 < nsteps) {
-      wait_fetch(step + 1, issued);
-      // this wave's reads of step `step` are complete (their registers are
-      // about to be consumed), so after the barrier its stage may be refilled
-      __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
-      __syncthreads();
-      if (step + C::Stages < nsteps) {
-        fetch(step + C::Stages);
-        ++issued;
+  read_half(0, fa[0], fb[0]);
+  auto iteration = [&](int h, bf16x8 (&ca)[2][C::RB], bf16x8 (&cb)[2][C::CB],
+                       bf16x8 (&na)[2][C::RB], bf16x8 (&nb)[2][C::CB]) {
+    if (h + 1 < nh) {
+      if ((h + 1) % kHS == 0) {
+        const int t = (h + 1) / kHS;
+        wait_fetch(t, issued);
+        // this wave's reads of step t - 1 are complete (their registers are
+        // about to be consumed), so after the barrier its stage may be refilled
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+        __syncthreads();
+        if (t - 1 + C::Stages < nsteps) {
+          fetch(t - 1 + C::Stages);
+          ++issued;
+        }
       }
-      read_frags(step + 1, na, nb);
+      read_half(h + 1, na, nb);
     }
     mfmas(ca, cb);
   };
-  int step = 0;
-  for (; step + 1 < nsteps; step += 2) {
-    iteration(step, fa[0], fb[0], fa[1], fb[1]);
-    iteration(step + 1, fa[1], fb[1], fa[0], fb[0]);
+  int h = 0;
+  for (; h + 1 < nh; h += 2) {
+    iteration(h, fa[0], fb[0], fa[1], fb[1]);
+    iteration(h + 1, fa[1], fb[1], fa[0], fb[0]);
   }
-  if (step < nsteps) iteration(step, fa[0], fb[0], fa[1], fb[1]);
+  if (h < nh) iteration(h, fa[0], fb[0], fa[1], fb[1]);
 
   // acc[rb][cb][i]: tile row RB*32 wm + 32 rb + 8 (i / 4) + 4 kh + i % 4,
   // column CB*32 wn + 32 cb + li.
@@ -230,9 +242,9 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
 
 // Cost of a launch = tiles per CU (workgroups / 256, rounded up) x the
 // measured time of one tile of the shape on MI355X (K = 2048): 256x256
-// 63 us, 128x256 38 us, 128x128 20.5 us (two per CU).  Fitted on
-// M = 512..8192 x N = 2048, 9216, 12352; it picks the fastest of the three
-// at each of those shapes.
+// 58 us, 128x256 35 us, 128x128 18 us (two per CU).  Fitted on
+// M = 1024..8192 x N = 2048, 9216; it picks the fastest of the three at each
+// of those shapes.
 template <class C>
 long long tile_cost(unsigned M, unsigned N, int tile_time) {
   const long long wgs = (long long)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
@@ -264,7 +276,7 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
                                         unsigned ldy, unsigned m, unsigned n, unsigned k,
                                         void* stream) {
   if (x == nullptr || w == nullptr || y == nullptr || m == 0 || n == 0 || k == 0 ||
-      m > kMaxTokens || n > 65536u || k > 16384u || (k % 32) != 0 || ldx < k ||
+      m > kMaxTokens || n > 65536u || k > 16384u || (k % 64) != 0 || ldx < k ||
       (ldx % 8) != 0 || ldy < n || !al16(x) || !al16(w) || (size_t)256 * ldx * 2 >= kGOob ||
       (size_t)256 * k * 2 >= kGOob)
     return Q36_EINVAL;
@@ -290,8 +302,8 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
   a.N = n;
   a.K = k;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const long long cl = tile_cost<CfgL>(m, n, 630), cm = tile_cost<CfgM>(m, n, 380),
-                  cs = tile_cost<CfgS>(m, n, 205);
+  const long long cl = tile_cost<CfgL>(m, n, 58), cm = tile_cost<CfgM>(m, n, 35),
+                  cs = tile_cost<CfgS>(m, n, 18);
   if (cl <= cm && cl <= cs) return launch_cfg<CfgL>(a, st);
   if (cm <= cs) return launch_cfg<CfgM>(a, st);
   return launch_cfg<CfgS>(a, st);

@@ -259,7 +259,7 @@ int qwen36_gdn_decode_step(const void* mixed_qkv, unsigned x_row_stride,
  * torch form `inp @ W.t()` in four_layer_mini_engine.py:6566-6573, :6386-6395,
  * :6653, :6544).  x row-major with row stride ldx (>= k, a multiple of 8), W
  * row-major [n, k] (out x in features), y row-major with row stride ldy
- * (>= n); x and W 16-byte aligned; k a multiple of 32 (<= 16384), n <= 65536,
+ * (>= n); x and W 16-byte aligned; k a multiple of 64 (<= 16384), n <= 65536,
  * m <= 262144. */
 int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y,
                              unsigned ldy, unsigned m, unsigned n, unsigned k,

@@ -15,7 +15,7 @@ def _check(y, ref):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 32, 2048), (37, 9216, 2048), (300, 2048, 4096),
-                                   (1024, 12352, 2048), (777, 512, 2048), (129, 300, 96),
+                                   (1024, 12352, 2048), (777, 512, 2048), (129, 300, 128),
                                    (8192, 2048, 4096)])
 def test_prefill_gemm_matches_fp32(gpu, m, n, k):
     from qwen36_attn.prefill_gemm import linear
@@ -49,7 +49,7 @@ def test_prefill_gemm_rejects_bad_shapes(gpu):
     w = torch.zeros(8, 2048, dtype=torch.bfloat16, device=gpu)
     y = torch.zeros(4, 8, dtype=torch.bfloat16, device=gpu)
     call = lambda *a: lib.qwen36_prefill_gemm_bf16(*a, None)
-    assert call(x.data_ptr(), 2048, w.data_ptr(), y.data_ptr(), 8, 4, 8, 2000) == 1   # k % 32
+    assert call(x.data_ptr(), 2048, w.data_ptr(), y.data_ptr(), 8, 4, 8, 2000) == 1   # k % 64
     assert call(x.data_ptr(), 2000, w.data_ptr(), y.data_ptr(), 8, 4, 8, 2048) == 1   # ldx < k
     assert call(x.data_ptr(), 2048, w.data_ptr(), y.data_ptr(), 4, 4, 8, 2048) == 1   # ldy < n
     assert call(x.data_ptr() + 2, 2048, w.data_ptr(), y.data_ptr(), 8, 4, 8, 2048) == 1
