@@ -90,6 +90,12 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
   for (unsigned t = 0; t < tokens; ++t) {
     const int par = t & 1;
+    // z of this token for the gated norm (wave 0, lanes 0..31), requested
+    // with the token's other inputs so its round trip is not paid after
+    // the delta rule
+    bf16x4 zrow;
+    if (wave == 0 && lane < 32)
+      zrow = *reinterpret_cast<const bf16x4*>(z + (size_t)t * z_row_stride + h * kGdnDv + 4 * cq);
     // -- phase A: conv + SiLU (bf16-rounded, as the conv kernel), gating --
     if (conv_thread) {
       const float cur = bf2f(x[(size_t)t * x_row_stride + ch]);
@@ -177,12 +183,11 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
       for (int off = 16; off > 0; off >>= 1) ss = ds_add(ss, __shfl_xor(ss, off, 64));
       const float inv = (float)(1.0 / sqrt((double)ds_add(ds_mul(ss, 1.0f / 128.0f), 1e-6f)));
       if (lane < 32) {
-        const bf16* zp = z + (size_t)t * z_row_stride + h * kGdnDv + 4 * cq;
         bf16x4 res;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float nv = bf2f(f2bf(ds_mul(ds_mul(ob[e], inv), nw[e])));
-          const float zv = bf2f(zp[e]);
+          const float zv = bf2f(zrow[e]);
           const float silu = zv / (1.0f + expf(-zv));
           res[e] = f2bf(ds_mul(nv, silu));
         }
