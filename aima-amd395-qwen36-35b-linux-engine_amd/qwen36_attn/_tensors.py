@@ -28,6 +28,10 @@ def require(t: torch.Tensor, name: str, dtype: torch.dtype, shape=None,
 
 
 _SCRATCH: dict[tuple[str, int], torch.Tensor] = {}
+# Buffers replaced by a larger one stay allocated: a HIP graph captured
+# earlier may still hold their addresses, and freeing them would let the
+# allocator hand that memory to other tensors which a replay then overwrites.
+_RETIRED: list[torch.Tensor] = []
 
 
 def scratch(tag: str, nbytes: int, device: torch.device) -> torch.Tensor:
@@ -35,10 +39,18 @@ def scratch(tag: str, nbytes: int, device: torch.device) -> torch.Tensor:
     when first allocated; the kernels write every workspace byte they read, so
     no call depends on what an earlier call left there).  Calls that share a
     tag on one device share the buffer, so they are ordered by the stream they
-    run on."""
+    run on.  A buffer is never freed once handed out; growing one during
+    graph capture is refused (make one eager call of the same size before
+    capturing, as warm-up)."""
     key = (tag, device.index if device.index is not None else torch.cuda.current_device())
     buf = _SCRATCH.get(key)
     if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(
+                f"scratch '{tag}' would grow to {int(nbytes)} bytes during graph capture; "
+                "run the call once eagerly with the same sizes before capturing")
+        if buf is not None:
+            _RETIRED.append(buf)
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _SCRATCH[key] = buf
     return buf
