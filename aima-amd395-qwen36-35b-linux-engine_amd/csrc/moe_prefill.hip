@@ -374,8 +374,13 @@ struct GemmArgs {
   unsigned T, E, ld_out, max_items;
 };
 
+// The leading s_nop covers a hazard the compiler cannot see through the
+// inline assembly: the resource SGPRs (and m0) are written by VALU
+// readfirstlane / SALU instructions right before, and a VMEM instruction
+// reading an SGPR that a VALU wrote needs 5 wait states on gfx950 (issued
+// earlier, it reads the old descriptor).
 __device__ __forceinline__ void fetch_rows(unsigned lds_addr, int voff, const u32x4& rsrc) {
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds"
+  asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                :: "v"(voff), "s"(rsrc), "{m0}"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory");
 }
