@@ -185,4 +185,62 @@ __device__ __forceinline__ void gemm_mainloop(char* lds, const FetchPlan<C>& fp,
   if (h < nh) iteration(h, fa[0], fb[0], fa[1], fb[1]);
 }
 
+// Epilogue through LDS (after the K loop; the ring is free once every wave
+// has passed the barrier at its start): each wave stages its RB*32 x CB*32
+// sub-tile as bf16 rows in a private LDS region -- lanes 2j and 2j+1 swap
+// one value each (DPP) so that every LDS write is a dword of two adjacent
+// columns -- and then writes whole 16-byte row chunks to y (full 128-byte
+// lines for CB = 2), 8x fewer store instructions than one per element.
+// y points at the tile's origin (row stride ldy, a multiple of 8 elements,
+// 16-byte aligned); rows / cols are the valid extents of the tile.
+template <class C>
+__device__ __forceinline__ void gemm_store_tile_lds(char* lds, const f32x16 (&acc)[C::RB][C::CB],
+                                                    bf16* y, size_t ldy, int rows, int cols) {
+  constexpr int kRows = C::RB * 32, kCols = C::CB * 32, kPitch = kCols * 2;
+  static_assert(C::Waves * kRows * kPitch <= C::Lds, "staging fits the ring");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wm = wave % C::WM, wn = wave / C::WM;
+  const int li = lane & 31, kh = lane >> 5, odd = li & 1;
+  char* base = lds + wave * kRows * kPitch;
+  __syncthreads();
+#pragma unroll
+  for (int rb = 0; rb < C::RB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < C::CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; i += 2) {
+        // rows lr (value i) and lr + 1 (value i + 1) of column 32 cb + li
+        const int lr = 32 * rb + 8 * (i >> 2) + 4 * kh + (i & 3);
+        const unsigned a = __builtin_bit_cast(unsigned short, f2bf(acc[rb][cb][i]));
+        const unsigned b = __builtin_bit_cast(unsigned short, f2bf(acc[rb][cb][i + 1]));
+        // even lane keeps row lr and takes its odd neighbour's value of that
+        // row; odd lane keeps row lr + 1 and takes the even neighbour's
+        const unsigned give = odd ? a : b;
+        const unsigned got = (unsigned)__builtin_amdgcn_mov_dpp((int)give, 0xB1, 0xF, 0xF, false);
+        const unsigned word = odd ? (got | (b << 16)) : (a | (got << 16));
+        const int row = lr + odd, col = 32 * cb + li - odd;
+        *reinterpret_cast<unsigned*>(base + row * kPitch + col * 2) = word;
+      }
+  // the wave reads back only its own region, so no barrier is needed
+  constexpr int kChunks = kPitch / 16;            // 16-byte chunks per row
+  constexpr int kRowsPer = 64 / kChunks;          // rows per read instruction
+  const int r_base = kRows * wm, c_base = kCols * wn;
+#pragma unroll
+  for (int it = 0; it < kRows / kRowsPer; ++it) {
+    const int lr = it * kRowsPer + lane / kChunks, ch = lane % kChunks;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(base + lr * kPitch + ch * 16);
+    const int r = r_base + lr, c = c_base + 8 * ch;
+    if (r >= rows) continue;
+    bf16* yr = y + (size_t)r * ldy + c;
+    if (c + 8 <= cols) {
+      *reinterpret_cast<u32x4*>(yr) = v;
+    } else {
+      const bf16x8 e = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (c + k < cols) yr[k] = e[k];
+    }
+  }
+}
+
 }  // namespace q36

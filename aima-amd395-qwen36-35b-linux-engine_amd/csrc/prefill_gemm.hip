@@ -37,7 +37,10 @@ struct GemmArgs {
   unsigned m_tiles, n_tiles, share;
 };
 
-template <class C>
+// kVec: y 16-byte aligned and ldy % 8 == 0, so the tile leaves through LDS
+// as 16-byte row chunks (gemm_store_tile_lds); otherwise one bf16 store per
+// element.
+template <class C, bool kVec>
 __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(GemmArgs p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   // item -> (row tile, column tile): XCD x = blockIdx % 8 takes items
@@ -86,6 +89,10 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
     for (int j = 0; j < C::CB; ++j) acc[i][j] = f32x16{};
   gemm_mainloop<C>(lds, fp, (int)p.K, arow, brow, acc);
 
+  if constexpr (kVec) {
+    gemm_store_tile_lds<C>(lds, acc, p.y + (size_t)row0 * p.ldy + n0, p.ldy, rows, cols);
+    return;
+  }
   // acc[rb][cb][i]: tile row RB*32 wm + 32 rb + 8 (i / 4) + 4 kh + i % 4,
   // column CB*32 wn + 32 cb + li.
 #pragma unroll
@@ -118,13 +125,13 @@ std::once_flag g_gemm_attr_once;
 hipError_t g_gemm_attr_status = hipSuccess;
 
 template <class C>
-int launch_cfg(const GemmArgs& base, hipStream_t stream) {
+int launch_cfg(const GemmArgs& base, bool vec, hipStream_t stream) {
   GemmArgs a = base;
   a.m_tiles = (a.M + C::BM - 1) / C::BM;
   a.n_tiles = (a.N + C::BN - 1) / C::BN;
   a.share = (a.m_tiles * a.n_tiles + 7) / 8;
-  hipLaunchKernelGGL(prefill_gemm_kernel<C>, dim3(8 * a.share), dim3(64 * C::Waves), C::Lds,
-                     stream, a);
+  auto kernel = vec ? prefill_gemm_kernel<C, true> : prefill_gemm_kernel<C, false>;
+  hipLaunchKernelGGL(kernel, dim3(8 * a.share), dim3(64 * C::Waves), C::Lds, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -145,9 +152,12 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
     return Q36_EINVAL;
   std::call_once(g_gemm_attr_once, [] {
     const std::pair<const void*, int> fs[] = {
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL>), CfgL::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM>), CfgM::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS>), CfgS::Lds}};
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, true>), CfgL::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, true>), CfgM::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, true>), CfgS::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, false>), CfgL::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, false>), CfgM::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, false>), CfgS::Lds}};
     for (const auto& f : fs) {
       const hipError_t e =
           hipFuncSetAttribute(f.first, hipFuncAttributeMaxDynamicSharedMemorySize, f.second);
@@ -164,10 +174,11 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
   a.M = m;
   a.N = n;
   a.K = k;
+  const bool vec = (ldy % 8) == 0 && al16(y);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const long long cl = tile_cost<CfgL>(m, n, 58), cm = tile_cost<CfgM>(m, n, 35),
                   cs = tile_cost<CfgS>(m, n, 18);
-  if (cl <= cm && cl <= cs) return launch_cfg<CfgL>(a, st);
-  if (cm <= cs) return launch_cfg<CfgM>(a, st);
-  return launch_cfg<CfgS>(a, st);
+  if (cl <= cm && cl <= cs) return launch_cfg<CfgL>(a, vec, st);
+  if (cm <= cs) return launch_cfg<CfgM>(a, vec, st);
+  return launch_cfg<CfgS>(a, vec, st);
 }
