@@ -276,8 +276,8 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 1);
   }
   l += __shfl_xor(l, 32, 64);
-  if (!row_valid) return;
   if constexpr (kSplit) {
+    if (!row_valid) return;
     const size_t item = ((size_t)qtile * sp.n_chunks + chunk) * kHq + head;
     const unsigned r = row - q0;
     float* op = sp.o + (item * kFmRows + r) * kD + 4 * lg;
@@ -289,16 +289,41 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
             f32x4{o[dt][4 * r4], o[dt][4 * r4 + 1], o[dt][4 * r4 + 2], o[dt][4 * r4 + 3]};
     if (lg == 0) *reinterpret_cast<float2*>(sp.ml + (item * kFmRows + r) * 2) = float2{m, l};
     return;
-  }
-  const float inv = 1.0f / l;
-  float* op = out + (size_t)row * kQDim + head * kD + 4 * lg;
+  } else {
+    // The output leaves through LDS in four rounds of 64 dims: each wave
+    // stages its 32 rows x 64 dims (8 KiB, 16-byte chunks XOR-swizzled by
+    // row so both the staging writes and the row reads are conflict-free)
+    // and stores whole 256-byte row segments, instead of 32-byte pieces of
+    // 32 rows per store instruction.
+    const float inv = row_valid ? 1.0f / l : 0.f;
+    __syncthreads();   // every wave is done with the K/V ring
+    char* stg = lds + wave * 8192;
+    const unsigned wrow0 = q0 + wave * kFmRowsPerWave;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
+    for (int rd = 0; rd < 4; ++rd) {
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      f32x4 val = {o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv,
-                   o[dt][4 * r4 + 2] * inv, o[dt][4 * r4 + 3] * inv};
-      *reinterpret_cast<f32x4*>(op + dt * 32 + 8 * r4) = val;
+      for (int d2 = 0; d2 < 2; ++d2) {
+        const int dt = 2 * rd + d2;
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int ch = d2 * 8 + 2 * r4 + lg;   // dims 4 ch .. 4 ch + 3 of the round
+          *reinterpret_cast<f32x4*>(stg + lj * 256 + ((ch ^ (lj & 15)) * 16)) =
+              f32x4{o[dt][4 * r4] * inv, o[dt][4 * r4 + 1] * inv, o[dt][4 * r4 + 2] * inv,
+                    o[dt][4 * r4 + 3] * inv};
+        }
+      }
+      // this wave's staging writes land before its reads (and its reads
+      // before the next round's writes): LDS serves one wave in order
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int r = it * 4 + (lane >> 4), ch = lane & 15;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((ch ^ (r & 15)) * 16));
+        if (wrow0 + r < q_tokens)
+          *reinterpret_cast<f32x4*>(out + (size_t)(wrow0 + r) * kQDim + head * kD + rd * 64 +
+                                    ch * 4) = v;
+      }
+      __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
   }
 }
