@@ -183,6 +183,8 @@ def test_short_prefills_on_two_streams(gpu):
             for (q, k, v), s in zip(dev, streams):
                 out = torch.full((q.shape[0], 4096), float("nan"), device=gpu)
                 with torch.cuda.stream(s):
+                    # the NaN fill ran on the default stream: order it first
+                    s.wait_stream(torch.cuda.default_stream(gpu))
                     h = s.cuda_stream
                     if form == "provider":
                         rc = lib.qrt_ck_fmha_bf16_launch_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(),
