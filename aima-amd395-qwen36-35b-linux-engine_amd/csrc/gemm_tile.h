@@ -189,18 +189,21 @@ __device__ __forceinline__ void gemm_mainloop(char* lds, const FetchPlan<C>& fp,
 // has passed the barrier at its start): each wave stages its RB*32 x CB*32
 // sub-tile as bf16 rows in a private LDS region -- lanes 2j and 2j+1 swap
 // one value each (DPP) so that every LDS write is a dword of two adjacent
-// columns -- and then writes whole 16-byte row chunks to y (full 128-byte
-// lines for CB = 2), 8x fewer store instructions than one per element.
-// y points at the tile's origin (row stride ldy, a multiple of 8 elements,
-// 16-byte aligned); rows / cols are the valid extents of the tile.
-template <class C>
+// columns -- and then writes whole 16-byte row chunks (full 128-byte lines
+// for CB = 2), 8x fewer store instructions than one per element.
+// val(x, r) rounds accumulator x of tile row r to the stored bf16;
+// row_ptr(r) is the destination of tile row r at the tile's first column
+// (16-byte aligned), or nullptr for a row that is not stored; cols is the
+// number of valid tile columns.
+template <class C, class RowPtr, class Val>
 __device__ __forceinline__ void gemm_store_tile_lds(char* lds, const f32x16 (&acc)[C::RB][C::CB],
-                                                    bf16* y, size_t ldy, int rows, int cols) {
+                                                    int cols, RowPtr row_ptr, Val val) {
   constexpr int kRows = C::RB * 32, kCols = C::CB * 32, kPitch = kCols * 2;
   static_assert(C::Waves * kRows * kPitch <= C::Lds, "staging fits the ring");
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int wm = wave % C::WM, wn = wave / C::WM;
   const int li = lane & 31, kh = lane >> 5, odd = li & 1;
+  const int r_base = kRows * wm, c_base = kCols * wn;
   char* base = lds + wave * kRows * kPitch;
   __syncthreads();
 #pragma unroll
@@ -211,8 +214,9 @@ __device__ __forceinline__ void gemm_store_tile_lds(char* lds, const f32x16 (&ac
       for (int i = 0; i < 16; i += 2) {
         // rows lr (value i) and lr + 1 (value i + 1) of column 32 cb + li
         const int lr = 32 * rb + 8 * (i >> 2) + 4 * kh + (i & 3);
-        const unsigned a = __builtin_bit_cast(unsigned short, f2bf(acc[rb][cb][i]));
-        const unsigned b = __builtin_bit_cast(unsigned short, f2bf(acc[rb][cb][i + 1]));
+        const unsigned a = __builtin_bit_cast(unsigned short, val(acc[rb][cb][i], r_base + lr));
+        const unsigned b =
+            __builtin_bit_cast(unsigned short, val(acc[rb][cb][i + 1], r_base + lr + 1));
         // even lane keeps row lr and takes its odd neighbour's value of that
         // row; odd lane keeps row lr + 1 and takes the even neighbour's
         const unsigned give = odd ? a : b;
@@ -224,21 +228,20 @@ __device__ __forceinline__ void gemm_store_tile_lds(char* lds, const f32x16 (&ac
   // the wave reads back only its own region, so no barrier is needed
   constexpr int kChunks = kPitch / 16;            // 16-byte chunks per row
   constexpr int kRowsPer = 64 / kChunks;          // rows per read instruction
-  const int r_base = kRows * wm, c_base = kCols * wn;
 #pragma unroll
   for (int it = 0; it < kRows / kRowsPer; ++it) {
     const int lr = it * kRowsPer + lane / kChunks, ch = lane % kChunks;
     const u32x4 v = *reinterpret_cast<const u32x4*>(base + lr * kPitch + ch * 16);
-    const int r = r_base + lr, c = c_base + 8 * ch;
-    if (r >= rows) continue;
-    bf16* yr = y + (size_t)r * ldy + c;
+    bf16* yr = row_ptr(r_base + lr);
+    const int c = c_base + 8 * ch;
+    if (yr == nullptr) continue;
     if (c + 8 <= cols) {
-      *reinterpret_cast<u32x4*>(yr) = v;
+      *reinterpret_cast<u32x4*>(yr + c) = v;
     } else {
       const bf16x8 e = __builtin_bit_cast(bf16x8, v);
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (c + k < cols) yr[k] = e[k];
+        if (c + k < cols) yr[c + k] = e[k];
     }
   }
 }

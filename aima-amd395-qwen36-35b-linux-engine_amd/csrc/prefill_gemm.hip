@@ -90,7 +90,10 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
   gemm_mainloop<C>(lds, fp, (int)p.K, arow, brow, acc);
 
   if constexpr (kVec) {
-    gemm_store_tile_lds<C>(lds, acc, p.y + (size_t)row0 * p.ldy + n0, p.ldy, rows, cols);
+    bf16* y0 = p.y + (size_t)row0 * p.ldy + n0;
+    gemm_store_tile_lds<C>(
+        lds, acc, cols, [&](int r) { return r < rows ? y0 + (size_t)r * p.ldy : nullptr; },
+        [](float x, int) { return f2bf(x); });
     return;
   }
   // acc[rb][cb][i]: tile row RB*32 wm + 32 rb + 8 (i / 4) + 4 kh + i % 4,
