@@ -14,8 +14,13 @@
 //    serves one head); the cache's 32-token blocks are dealt to
 //    the splits round-robin (and to the 4 waves of a split in turn), so the
 //    grid sweeps the cache as one contiguous window.
-//  * per block: S^T = K Q^T on MFMA 16x16x32 (A = K streamed from HBM into
-//    registers, B = the 8 query heads of the group, padded to 16 columns),
+//  * K and V are read as whole 512-byte half-rows (two rows per load
+//    instruction) by unconditional buffer loads -- rows past cache_end read
+//    as zeros, so no load sits in a branch and the compiler's in-order wait
+//    counts keep the next block's loads in flight; K then passes through
+//    the wave's LDS slot into the MFMA operand layout.
+//  * per block: S^T = K Q^T on MFMA 16x16x32 (A = K from LDS, B = the 8
+//    query heads of the group, padded to 16 columns),
 //    online softmax per head in fp32 (exp2 domain), then O^T += V^T P^T on
 //    MFMA with V staged row-major in LDS and read transposed with
 //    ds_read_b64_tr_b16.  The P^T operand is the S^T accumulator itself
@@ -40,7 +45,9 @@ constexpr int kDecBlock = 32;          // tokens per wave iteration
 constexpr int kVPitch = 544;           // LDS row pitch in bytes (512 + 32)
 constexpr int kVLds = kDecWaves * kDecBlock * kVPitch;   // 69632 bytes
 constexpr int kQPitch = 528;           // LDS row pitch of the Q^T operand
-constexpr int kDecLds = kVLds + 16 * kQPitch;            // 78080 bytes
+constexpr int kKPitch = 528;           // LDS row pitch of the staged K rows
+constexpr int kKLds = kDecWaves * kDecBlock * kKPitch;   // 67584 bytes
+constexpr int kDecLds = kVLds + kKLds + 16 * kQPitch;    // 145664 bytes
 
 constexpr unsigned kMaxSplits = 256;
 // Default split count: 128 splits x 2 KV heads = one workgroup per CU.
@@ -81,7 +88,7 @@ __device__ __forceinline__ void store_partial(float* o, float* ml,
 }
 
 template <bool kFuse>
-__global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
+__global__ __launch_bounds__(256, 1) void decode_gqa_split_kernel(
     const bf16* __restrict__ q, bf16* __restrict__ k_cache,
     bf16* __restrict__ v_cache, const bf16* __restrict__ k_new,
     const bf16* __restrict__ v_new, unsigned position, unsigned cache_end,
@@ -104,19 +111,17 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // each row at about the same time), which keeps HBM pages and channels
   // evenly and sequentially used.
   const unsigned end = cache_end;
-  // The workgroup that owns the new row's block writes it to the cache (this
-  // KV head's half) and reads K/V for that token from k_new/v_new directly,
-  // so no other workgroup depends on the write.
+  // The workgroup that owns the new row's block writes the row into the
+  // cache (this KV head's half: the copy of k_new / v_new, or in the fused
+  // step K after head norm and RoPE and V raw) and is its only reader, so it
+  // then streams that row from the cache like every other.  If the row lies
+  // in one of the first blocks (round < 4: short caches) the write completes
+  // before any load is issued; otherwise it overlaps the first loads and the
+  // workgroup barrier after Q staging orders it before the row's block is
+  // read.  Raw inputs of the fused step are requested before the first K/V
+  // block so that their (short) round trip does not queue behind it.
   const bool owner = (position / kDecBlock) % nsplit == split;
-  const bool has_new = !kFuse && k_new != nullptr && owner;
-  // Fused step: the owner writes the new row -- K after head norm and RoPE,
-  // V raw -- and is its only reader, so it then streams that row from the
-  // cache like every other.  If the row lies in one of the first blocks
-  // (round < 4: short caches) the write completes before any load is issued;
-  // otherwise it overlaps the first loads and the workgroup barrier after Q
-  // staging orders it before the row's block is read.
-  // Raw inputs of the fused step are requested before the first K/V block so
-  // that their (short) round trip does not queue behind it.
+  const bool new_row = owner && (kFuse || k_new != nullptr);
   float xq[2][4], xk[4];
   bf16x4 vrow;
   if constexpr (kFuse) {
@@ -136,34 +141,34 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   }
   auto write_new_row = [&]() {
     const size_t o = ((size_t)position * kHkv + kvh) * kD;
-    if (wave == 0) {
-      float y[4];
-      float cs[4], sn[4];
-      rope_cos_sin_wave(position, c_dec_inv_freq, cs, sn);
-      head_norm_rope_wave(xk, fz.k_w, cs, sn, y);
-      bf16x4 yb;
+    if constexpr (kFuse) {
+      if (wave == 0) {
+        float y[4];
+        float cs[4], sn[4];
+        rope_cos_sin_wave(position, c_dec_inv_freq, cs, sn);
+        head_norm_rope_wave(xk, fz.k_w, cs, sn, y);
+        bf16x4 yb;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) yb[e] = f2bf(y[e]);
-      *reinterpret_cast<bf16x4*>(k_cache + o + 4 * lane) = yb;
-    } else if (wave == 1) {
-      *reinterpret_cast<bf16x4*>(v_cache + o + 4 * lane) = vrow;
+        for (int e = 0; e < 4; ++e) yb[e] = f2bf(y[e]);
+        *reinterpret_cast<bf16x4*>(k_cache + o + 4 * lane) = yb;
+      } else if (wave == 1) {
+        *reinterpret_cast<bf16x4*>(v_cache + o + 4 * lane) = vrow;
+      }
+    } else if (wave == 0) {
+      if (lane < 32) {
+        reinterpret_cast<uint4*>(k_cache + o)[lane] =
+            reinterpret_cast<const uint4*>(k_new + kvh * kD)[lane];
+      } else {
+        reinterpret_cast<uint4*>(v_cache + o)[lane - 32] =
+            reinterpret_cast<const uint4*>(v_new + kvh * kD)[lane - 32];
+      }
     }
   };
-  const bool early_row = kFuse && owner && (position / kDecBlock) / nsplit < (unsigned)kDecWaves;
+  const bool early_row = new_row && (position / kDecBlock) / nsplit < (unsigned)kDecWaves;
   if (early_row) {
     write_new_row();
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-  }
-  if (has_new && wave == 0) {
-    const size_t o = ((size_t)position * kHkv + kvh) * kD;
-    if (lane < 32) {
-      reinterpret_cast<uint4*>(k_cache + o)[lane] =
-          reinterpret_cast<const uint4*>(k_new + kvh * kD)[lane];
-    } else {
-      reinterpret_cast<uint4*>(v_cache + o)[lane - 32] =
-          reinterpret_cast<const uint4*>(v_new + kvh * kD)[lane - 32];
-    }
   }
 
 
@@ -177,41 +182,40 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // Software pipeline: the K fragments and V rows of the next block are
   // requested as soon as the registers holding the current block are free,
   // so HBM latency overlaps the softmax and PV work.
-  bf16x8 kf[2][8];
+  // K and V rows are both read as whole 512-byte half-rows (two rows per
+  // load instruction, every 128-byte line fully used); K then passes
+  // through this wave's LDS slot into the MFMA operand layout (16 rows x 64
+  // bytes per operand read).  Measured on MI355X with a read-only kernel
+  // over a 128K cache: reading K directly in the operand layout (16 rows x
+  // 64 bytes per load instruction, half lines) streams a layer in 41.8 us,
+  // whole half-rows in 38.8 us.
+  u32x4 kr[16];
   u32x4 vr[16];
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)k_cache, 0, (int)(end * (unsigned)kKvRow * 2u), 0x00020000);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)v_cache, 0, (int)(end * (unsigned)kKvRow * 2u), 0x00020000);
   auto load_k = [&](unsigned t0) {
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const unsigned tok = t0 + tt * 16 + li;
-      if (tok < end) {
-        const bf16* krow = (has_new && tok == position)
-                               ? k_new + kvh * kD
-                               : k_cache + ((size_t)tok * kHkv + kvh) * kD;
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-          kf[tt][s] = __builtin_bit_cast(
-              bf16x8, __builtin_nontemporal_load(
-                          reinterpret_cast<const u32x4*>(krow + 32 * s + 8 * lg)));
-      } else {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) kf[tt][s] = bf16x8{};
-      }
+    for (int c = 0; c < 16; ++c) {
+      const unsigned tok = t0 + 2 * c + (lane >> 5);
+      const int off = (int)(tok * (unsigned)kKvRow * 2u + kvh * kD * 2 + (lane & 31) * 16);
+      kr[c] = __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 2);
     }
+  };
+  char* kbuf = lds + kVLds + wave * kDecBlock * kKPitch;
+  auto stage_k = [&]() {
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+      *reinterpret_cast<u32x4*>(kbuf + (2 * c + (lane >> 5)) * kKPitch + (lane & 31) * 16) = kr[c];
   };
   // V rows: row = 2c + lane/32, 16-byte chunk = lane%32 (fully coalesced).
   auto load_v = [&](unsigned t0) {
 #pragma unroll
     for (int c = 0; c < 16; ++c) {
       const unsigned tok = t0 + 2 * c + (lane >> 5);
-      if (tok < end) {
-        const bf16* vrow = (has_new && tok == position)
-                               ? v_new + kvh * kD
-                               : v_cache + ((size_t)tok * kHkv + kvh) * kD;
-        vr[c] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(vrow + (lane & 31) * 8));
-      } else {
-        vr[c] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const int off = (int)(tok * (unsigned)kKvRow * 2u + kvh * kD * 2 + (lane & 31) * 16);
+      vr[c] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 2);
     }
   };
 
@@ -228,9 +232,10 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
   // block to free registers for the load pipeline.  Reduction step s covers
   // dims s*32 + 8*lg .. +8, so one K load instruction reads 16 rows x 64
   // contiguous bytes.
-  char* qs = lds + kVLds;
+  char* qs = lds + kVLds + kKLds;
+  const bool late_row = new_row && !early_row;
+  if (late_row) write_new_row();
   if constexpr (kFuse) {
-    if (owner && !early_row) write_new_row();
     // Head norm + RoPE of this group's 8 query heads (wave w: heads 2w,
     // 2w+1) straight into the Q^T operand rows; rows 8..15 are zero padding.
     float cs[4], sn[4];
@@ -249,7 +254,6 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
       const int r = kGroup + (threadIdx.x >> 5), c = threadIdx.x & 31;
       *reinterpret_cast<uint4*>(qs + r * kQPitch + c * 16) = uint4{0u, 0u, 0u, 0u};
     }
-    __builtin_amdgcn_s_waitcnt(0);   // the new row's stores complete before the barrier
   } else {
     const int r = threadIdx.x >> 4, c = threadIdx.x & 15;   // 16 rows x 16 chunks
     uint4 a = uint4{0u, 0u, 0u, 0u}, b = uint4{0u, 0u, 0u, 0u};
@@ -261,18 +265,26 @@ __global__ __launch_bounds__(256, 2) void decode_gqa_split_kernel(
     *reinterpret_cast<uint4*>(qs + r * kQPitch + c * 16) = a;
     *reinterpret_cast<uint4*>(qs + r * kQPitch + (c + 16) * 16) = b;
   }
+  // the new row's stores complete before the barrier (the waves that wrote)
+  if (late_row && wave < 2) __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const char* qrow = qs + li * kQPitch + lg * 16;
+  const char* krow0 = kbuf + li * kKPitch + lg * 16;
   for (; t0 < end; t0 += stride) {
     const unsigned tn = t0 + stride;
+    // K of this block into the operand layout; the next block's K is then
+    // requested at once (its registers are free)
+    stage_k();
+    if (tn < end) load_k(tn);
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const bf16x8 qf = *reinterpret_cast<const bf16x8*>(qrow + 64 * s);
-      s0 = mfma16x16x32(kf[0][s], qf, s0);
-      s1 = mfma16x16x32(kf[1][s], qf, s1);
+      const bf16x8 k0 = *reinterpret_cast<const bf16x8*>(krow0 + 64 * s);
+      const bf16x8 k1 = *reinterpret_cast<const bf16x8*>(krow0 + 16 * kKPitch + 64 * s);
+      s0 = mfma16x16x32(k0, qf, s0);
+      s1 = mfma16x16x32(k1, qf, s1);
     }
-    if (tn < end) load_k(tn);
     // Lane holds S^T[token t0 + 16*tt + 4*lg + r][head li].
     float sc[8];
 #pragma unroll
