@@ -33,24 +33,32 @@ struct GemmArgs {
   const bf16* x;
   const bf16* w;
   bf16* y;
+  float* part;          // split-K: fp32 partial products [ksplit][M][N]
   unsigned ldx, ldy, M, N, K;
   unsigned m_tiles, n_tiles, share;
+  unsigned ksplit, kslice;   // K is cut into ksplit slices of kslice
 };
 
-// kVec: y 16-byte aligned and ldy % 8 == 0, so the tile leaves through LDS
-// as 16-byte row chunks (gemm_store_tile_lds); otherwise one bf16 store per
-// element.
-template <class C, bool kVec>
+enum GemmOut { kOutBf16 = 0, kOutBf16Staged = 1, kOutPartial = 2 };
+
+// kOut: kOutBf16Staged when y is 16-byte aligned and ldy % 8 == 0 (the tile
+// leaves through LDS as 16-byte row chunks, gemm_store_tile_lds), kOutBf16
+// otherwise (one store per element), kOutPartial for a split-K slice (fp32
+// products into the slice's plane of p.part; gemm_splitk_reduce_kernel sums
+// the planes in slice order and rounds once).
+template <class C, int kOut>
 __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(GemmArgs p) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
-  // item -> (row tile, column tile): XCD x = blockIdx % 8 takes items
-  // [x * share, (x + 1) * share); items sweep groups of 8 row tiles per
-  // column tile.
-  const unsigned items = p.m_tiles * p.n_tiles;
+  // item -> (K slice, row tile, column tile): XCD x = blockIdx % 8 takes
+  // items [x * share, (x + 1) * share); within a K slice, items sweep groups
+  // of 8 row tiles per column tile.
+  const unsigned tiles = p.m_tiles * p.n_tiles;
+  const unsigned items = tiles * p.ksplit;
   const unsigned xi = blockIdx.x >> 3;
   if (xi >= p.share) return;
-  const unsigned item = (blockIdx.x & 7) * p.share + xi;
-  if (item >= items) return;
+  const unsigned item_all = (blockIdx.x & 7) * p.share + xi;
+  if (item_all >= items) return;
+  const unsigned ks = item_all / tiles, item = item_all % tiles;
   const unsigned grp = item / (8 * p.n_tiles), rem = item % (8 * p.n_tiles);
   const unsigned mg = min(8u, p.m_tiles - grp * 8);
   const unsigned nt = rem / mg, mt = grp * 8 + rem % mg;
@@ -69,7 +77,8 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
     const bool is_a = srow < C::BM;
     const int r = is_a ? srow : srow - C::BM;
     const bool live = is_a ? r < rows : r < cols;
-    const unsigned off = is_a ? (unsigned)r * p.ldx * 2u : (unsigned)r * p.K * 2u;
+    const unsigned off = (is_a ? (unsigned)r * p.ldx * 2u : (unsigned)r * p.K * 2u) +
+                         ks * p.kslice * 2u;
     fp.off[j] = live ? off + fetch_chunk_off<C>(srow, lane) : kGOob;
     const u32x4 rs = is_a ? ars : brs;
 #pragma unroll
@@ -87,9 +96,25 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
   for (int i = 0; i < C::RB; ++i)
 #pragma unroll
     for (int j = 0; j < C::CB; ++j) acc[i][j] = f32x16{};
-  gemm_mainloop<C>(lds, fp, (int)p.K, arow, brow, acc);
+  gemm_mainloop<C>(lds, fp, (int)p.kslice, arow, brow, acc);
 
-  if constexpr (kVec) {
+  if constexpr (kOut == kOutPartial) {
+    float* pp = p.part + (size_t)ks * p.M * p.N + (size_t)row0 * p.N + n0;
+#pragma unroll
+    for (int rb = 0; rb < C::RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int r = C::RB * 32 * wm + 32 * rb + 8 * (i >> 2) + 4 * kh + (i & 3);
+        if (r >= rows) continue;
+#pragma unroll
+        for (int cb = 0; cb < C::CB; ++cb) {
+          const int c = C::CB * 32 * wn + 32 * cb + li;
+          if (c < cols) pp[(size_t)r * p.N + c] = acc[rb][cb][i];
+        }
+      }
+    return;
+  }
+  if constexpr (kOut == kOutBf16Staged) {
     bf16* y0 = p.y + (size_t)row0 * p.ldy + n0;
     gemm_store_tile_lds<C>(
         lds, acc, cols, [&](int r) { return r < rows ? y0 + (size_t)r * p.ldy : nullptr; },
@@ -113,15 +138,59 @@ __global__ __launch_bounds__(64 * C::Waves, C::MINWG) void prefill_gemm_kernel(G
     }
 }
 
-// Cost of a launch = tiles per CU (workgroups / 256, rounded up) x the
-// measured time of one tile of the shape on MI355X (K = 2048): 256x256
-// 58 us, 128x256 35 us, 128x128 18 us (two per CU).  Fitted on
-// M = 1024..8192 x N = 2048, 9216; it picks the fastest of the three at each
-// of those shapes.
-template <class C>
-long long tile_cost(unsigned M, unsigned N, int tile_time) {
-  const long long wgs = (long long)((M + C::BM - 1) / C::BM) * ((N + C::BN - 1) / C::BN);
-  return (wgs + 255) / 256 * tile_time;
+// y[r][c] = bf16(sum over slices s = 0, 1, ... of part[s][r][c]): one
+// rounding, slices added in order (deterministic); 4 columns per thread.
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float* __restrict__ part,
+                                                                 unsigned ksplit, unsigned M,
+                                                                 unsigned N, bf16* __restrict__ y,
+                                                                 unsigned ldy) {
+  const unsigned n4 = (N + 3) / 4;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)M * n4) return;
+  const unsigned r = (unsigned)(idx / n4), c = (unsigned)(idx % n4) * 4;
+  const size_t plane = (size_t)M * N;
+  const float* src = part + (size_t)r * N + c;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (unsigned k = 0; k < ksplit; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (c + e < N) s[e] += src[k * plane + e];
+  bf16* yr = y + (size_t)r * ldy + c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c + e < N) yr[e] = f2bf(s[e]);
+}
+
+// Launch plan: tile shape and K split.  Cost = rounds of 256 workgroups x
+// the measured tile time (K = 2048: 256x256 58 us, 128x256 35 us, 128x128
+// 18 us, two per CU) scaled by the slice length, plus, for a split, the
+// fp32 partial planes written and read back (at ~5 TB/s) -- so short prompts
+// with a long K (the K = 4096 output projections at T = 1024 fill half the
+// GPU with whole-K tiles) spread K over more workgroups.
+struct GemmPlan {
+  int cfg;            // 0: 256x256, 1: 128x256, 2: 128x128
+  unsigned ksplit;
+};
+
+GemmPlan gemm_plan(unsigned M, unsigned N, unsigned K, bool allow_split) {
+  const int bm[3] = {CfgL::BM, CfgM::BM, CfgS::BM}, bn[3] = {CfgL::BN, CfgM::BN, CfgS::BN};
+  const double tt[3] = {58.0, 35.0, 18.0};
+  GemmPlan best{0, 1};
+  double best_cost = 1e30;
+  for (int c = 0; c < 3; ++c) {
+    const long long wgs = (long long)((M + bm[c] - 1) / bm[c]) * ((N + bn[c] - 1) / bn[c]);
+    for (unsigned s = 1; s <= 8; s *= 2) {
+      if (s > 1 && (!allow_split || (K / s) % 64 != 0 || K / s < 512)) continue;
+      const double rounds = (double)((wgs * s + 255) / 256);
+      double cost = rounds * tt[c] * ((double)K / s) / 2048.0;
+      if (s > 1) cost += (double)M * N * 4.0 * (2.0 * s) / 5.0e6;
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = GemmPlan{c, s};
+      }
+    }
+  }
+  return best;
 }
 
 std::once_flag g_gemm_attr_once;
@@ -132,10 +201,21 @@ int launch_cfg(const GemmArgs& base, bool vec, hipStream_t stream) {
   GemmArgs a = base;
   a.m_tiles = (a.M + C::BM - 1) / C::BM;
   a.n_tiles = (a.N + C::BN - 1) / C::BN;
-  a.share = (a.m_tiles * a.n_tiles + 7) / 8;
-  auto kernel = vec ? prefill_gemm_kernel<C, true> : prefill_gemm_kernel<C, false>;
+  a.share = (a.m_tiles * a.n_tiles * a.ksplit + 7) / 8;
+  auto kernel = a.ksplit > 1 ? prefill_gemm_kernel<C, kOutPartial>
+                : vec        ? prefill_gemm_kernel<C, kOutBf16Staged>
+                             : prefill_gemm_kernel<C, kOutBf16>;
   hipLaunchKernelGGL(kernel, dim3(8 * a.share), dim3(64 * C::Waves), C::Lds, stream, a);
+  if (a.ksplit > 1) {
+    const size_t n = (size_t)a.M * ((a.N + 3) / 4);
+    hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       stream, a.part, a.ksplit, a.M, a.N, a.y, a.ldy);
+  }
   return static_cast<int>(hipGetLastError());
+}
+
+size_t splitk_bytes(unsigned m, unsigned n, unsigned ksplit) {
+  return ksplit > 1 ? (size_t)ksplit * m * n * sizeof(float) : 0;
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
@@ -145,22 +225,29 @@ bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
 
 using namespace q36;
 
-Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y,
-                                        unsigned ldy, unsigned m, unsigned n, unsigned k,
-                                        void* stream) {
-  if (x == nullptr || w == nullptr || y == nullptr || m == 0 || n == 0 || k == 0 ||
-      m > kMaxTokens || n > 65536u || k > 16384u || (k % 64) != 0 || ldx < k ||
-      (ldx % 8) != 0 || ldy < n || !al16(x) || !al16(w) || (size_t)256 * ldx * 2 >= kGOob ||
-      (size_t)256 * k * 2 >= kGOob)
-    return Q36_EINVAL;
+namespace {
+
+bool gemm_args_ok(const void* x, unsigned ldx, const void* w, const void* y, unsigned ldy,
+                  unsigned m, unsigned n, unsigned k) {
+  return !(x == nullptr || w == nullptr || y == nullptr || m == 0 || n == 0 || k == 0 ||
+           m > kMaxTokens || n > 65536u || k > 16384u || (k % 64) != 0 || ldx < k ||
+           (ldx % 8) != 0 || ldy < n || !al16(x) || !al16(w) ||
+           (size_t)256 * ldx * 2 >= kGOob || (size_t)256 * k * 2 >= kGOob);
+}
+
+int gemm_run(const void* x, unsigned ldx, const void* w, void* y, unsigned ldy, unsigned m,
+             unsigned n, unsigned k, const GemmPlan& plan, float* part, void* stream) {
   std::call_once(g_gemm_attr_once, [] {
     const std::pair<const void*, int> fs[] = {
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, true>), CfgL::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, true>), CfgM::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, true>), CfgS::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, false>), CfgL::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, false>), CfgM::Lds},
-        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, false>), CfgS::Lds}};
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, kOutBf16>), CfgL::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, kOutBf16>), CfgM::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, kOutBf16>), CfgS::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, kOutBf16Staged>), CfgL::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, kOutBf16Staged>), CfgM::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, kOutBf16Staged>), CfgS::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgL, kOutPartial>), CfgL::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgM, kOutPartial>), CfgM::Lds},
+        {reinterpret_cast<const void*>(prefill_gemm_kernel<CfgS, kOutPartial>), CfgS::Lds}};
     for (const auto& f : fs) {
       const hipError_t e =
           hipFuncSetAttribute(f.first, hipFuncAttributeMaxDynamicSharedMemorySize, f.second);
@@ -172,16 +259,41 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
   a.x = static_cast<const bf16*>(x);
   a.w = static_cast<const bf16*>(w);
   a.y = static_cast<bf16*>(y);
+  a.part = part;
   a.ldx = ldx;
   a.ldy = ldy;
   a.M = m;
   a.N = n;
   a.K = k;
+  a.ksplit = plan.ksplit;
+  a.kslice = k / plan.ksplit;
   const bool vec = (ldy % 8) == 0 && al16(y);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const long long cl = tile_cost<CfgL>(m, n, 58), cm = tile_cost<CfgM>(m, n, 35),
-                  cs = tile_cost<CfgS>(m, n, 18);
-  if (cl <= cm && cl <= cs) return launch_cfg<CfgL>(a, vec, st);
-  if (cm <= cs) return launch_cfg<CfgM>(a, vec, st);
+  if (plan.cfg == 0) return launch_cfg<CfgL>(a, vec, st);
+  if (plan.cfg == 1) return launch_cfg<CfgM>(a, vec, st);
   return launch_cfg<CfgS>(a, vec, st);
+}
+
+}  // namespace
+
+Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y,
+                                        unsigned ldy, unsigned m, unsigned n, unsigned k,
+                                        void* stream) {
+  if (!gemm_args_ok(x, ldx, w, y, ldy, m, n, k)) return Q36_EINVAL;
+  return gemm_run(x, ldx, w, y, ldy, m, n, k, gemm_plan(m, n, k, false), nullptr, stream);
+}
+
+Q36_EXPORT size_t qwen36_prefill_gemm_workspace_bytes(unsigned m, unsigned n, unsigned k) {
+  if (m == 0 || n == 0 || k == 0 || (k % 64) != 0) return 0;
+  return splitk_bytes(m, n, gemm_plan(m, n, k, true).ksplit);
+}
+
+Q36_EXPORT int qwen36_prefill_gemm_bf16_ws(const void* x, unsigned ldx, const void* w, void* y,
+                                           unsigned ldy, unsigned m, unsigned n, unsigned k,
+                                           void* ws, size_t ws_bytes, void* stream) {
+  if (!gemm_args_ok(x, ldx, w, y, ldy, m, n, k)) return Q36_EINVAL;
+  GemmPlan plan = gemm_plan(m, n, k, true);
+  const size_t need = splitk_bytes(m, n, plan.ksplit);
+  if (need > 0 && (ws == nullptr || ws_bytes < need || !al16(ws))) return Q36_EINVAL;
+  return gemm_run(x, ldx, w, y, ldy, m, n, k, plan, static_cast<float*>(ws), stream);
 }

@@ -58,6 +58,9 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     # prefill projections
     "qwen36_prefill_gemm_bf16": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "qwen36_prefill_gemm_workspace_bytes": (_sz, [_u32, _u32, _u32]),
+    "qwen36_prefill_gemm_bf16_ws": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _sz,
+                                           _vp]),
     # decode projections
     "qwen36_gemv_bf16": (_i32, [_vp, _u32, _u32, _vp, _vp, _vp]),
     # MoE block

@@ -2,13 +2,18 @@
 y = x W^T for T tokens, the reference's ``inp @ weights[...].t()``
 (four_layer_mini_engine.py:6566-6573 full attention, :6386-6395 Gated
 DeltaNet), which its native prefill runs as hipBLASLt plans
-(native_full_prefill.hip.cpp:552-560)."""
+(native_full_prefill.hip.cpp:552-560).
+
+``linear`` calls the workspace form (``qwen36_prefill_gemm_bf16_ws``): for
+short prompts with a long K the library cuts K into slices whose fp32
+partial products go to the shared ``prefill_gemm`` scratch and are summed in
+slice order (deterministic, one rounding)."""
 from __future__ import annotations
 
 import torch
 
 from . import _lib
-from ._tensors import ptr, require, stream_handle
+from ._tensors import ptr, require, scratch, stream_handle
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -25,6 +30,9 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) ->
     require(out, "out", torch.bfloat16, contiguous=False)
     if out.shape != (t, n) or out.stride(1) != 1:
         raise ValueError("out must be [T, N] with unit inner stride")
-    _lib.call("qwen36_prefill_gemm_bf16", ptr(x), x.stride(0), ptr(w), ptr(out), out.stride(0),
-              t, n, k, stream_handle(x.device))
+    lib = _lib.load(("qwen36_prefill_gemm_bf16_ws",))
+    nb = lib.qwen36_prefill_gemm_workspace_bytes(t, n, k)
+    ws = scratch("prefill_gemm", nb, x.device) if nb else None
+    _lib.call("qwen36_prefill_gemm_bf16_ws", ptr(x), x.stride(0), ptr(w), ptr(out), out.stride(0),
+              t, n, k, ptr(ws), ws.numel() if ws is not None else 0, stream_handle(x.device))
     return out

@@ -265,6 +265,22 @@ int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y
                              unsigned ldy, unsigned m, unsigned n, unsigned k,
                              void* stream);
 
+/* qwen36_prefill_gemm_workspace_bytes / qwen36_prefill_gemm_bf16_ws: the
+ * same product with a caller workspace, which lets a short prompt with a long
+ * k (e.g. the k = 4096 output projections at m = 1024, where whole-k tiles
+ * fill half the GPU) split k into slices: each slice's fp32 partial products
+ * go to the workspace and a second launch sums them in slice order and rounds
+ * once, so the result is deterministic; it can differ from
+ * qwen36_prefill_gemm_bf16's by the fp32 summation order (well inside one
+ * bf16 rounding).  workspace_bytes returns 0 when the shape runs unsplit (ws
+ * may then be NULL); otherwise ws is 16-byte aligned and holds at least that
+ * many bytes, else the call returns the invalid-argument code.  Same
+ * reference call sites as qwen36_prefill_gemm_bf16. */
+size_t qwen36_prefill_gemm_workspace_bytes(unsigned m, unsigned n, unsigned k);
+int qwen36_prefill_gemm_bf16_ws(const void* x, unsigned ldx, const void* w, void* y,
+                                unsigned ldy, unsigned m, unsigned n, unsigned k,
+                                void* ws, size_t ws_bytes, void* stream);
+
 /* ---- decode projections ----------------------------------------------------
  * qwen36_gemv_bf16: y[N] = W[N,K] x[K] for one token, bf16 in and out with
  * fp32 accumulation; replaces the decode projection GEMVs

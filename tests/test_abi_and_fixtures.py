@@ -126,6 +126,15 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 0, 16, 16, ws, None) == 1
     assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 16, 16, 16, ws - 1, None) == 1
     assert L.qwen36_moe_prefill(16, 16, 16, 16, 16, 16, 16, 256, 16, 18, 16, ws, None) == 1
+    # prefill GEMM workspace: split planes (a whole number of fp32 [m, n]
+    # planes) only for short prompts; 0 for long prompts and invalid k
+    G = L.qwen36_prefill_gemm_workspace_bytes
+    assert G(8192, 2048, 4096) == 0 and G(1024, 9216, 2048) == 0
+    assert G(1024, 2048, 4096) == 2 * 1024 * 2048 * 4
+    assert G(256, 2048, 4096) % (256 * 2048 * 4) == 0 and G(256, 2048, 4096) > 0
+    assert G(1024, 2048, 4000) == 0 and G(0, 2048, 4096) == 0
+    assert L.qwen36_prefill_gemm_bf16_ws(16, 2048, 16, 16, 2048, 300, 2048, 4096,
+                                         16, G(300, 2048, 4096) - 16, None) == 1
 
 
 def test_prefix_cache_host_bookkeeping_without_device(lib):
