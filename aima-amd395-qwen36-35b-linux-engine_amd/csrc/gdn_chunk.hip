@@ -24,19 +24,27 @@
 // Qg S = diag(qinv e^G / sqrt(128)) (q_raw S),
 // Kd^T v' = k_raw^T (diag(kinv e^(G_last - G)) v').
 //
+// The decomposition used by the two kernels below:
+//   W S = T diag(beta e^G kinv) (k_raw S)   and   U = T diag(beta) v, so
+//   v' = U - W S = (T diag(beta)) (v - diag(e^G kinv) (k_raw S)),
+//   Aqk = diag(qinv / sqrt(128)) (q_raw k_raw^T) diag(kinv) (.) exp(G_i - G_j).
+//
 // Two kernels:
-//  * gdn_chunk_prep (grid = chunks x 32 heads): everything independent of S
-//    -- U (fp32), W and Aqk (hi/lo bf16), the two row scales and
-//    exp(G_last) -- into the workspace.  T = (I+L)^-1 is formed blockwise:
-//    16x16 diagonal blocks by forward substitution, off-diagonal blocks by
-//    fp32 MFMA products.  LDS is kept near 72 KB so two workgroups share a CU.
+//  * gdn_chunk_prep (grid = chunks x 32 heads): the state-independent part
+//    that is sequential inside a chunk -- T = (I+L)^-1, formed blockwise
+//    (16x16 diagonal blocks by forward substitution, off-diagonal blocks by
+//    fp32 MFMA products) -- stored as T diag(beta) in hi/lo bf16 A-operand
+//    fragments, plus the chunk's per-token scalars (G, kinv, q scale, row
+//    scales, exp(G_last)): an 18 KB record per (chunk, head).
 //  * gdn_chunk_scan (grid = 32 heads x 8 groups of 16 v-columns, sequential
-//    over chunks): wave w owns token tile w of each chunk and state rows
-//    32w .. 32w+31 of its 16 columns, in registers in the MFMA accumulator
-//    layout.  That layout is also the B-operand layout of the next products
-//    (the reduction index -- state row or token -- is permuted to match, and
-//    prep stores the A operands in the same order, fragment-major), so per
-//    chunk only the state tiles and v' (hi/lo bf16) pass through LDS.
+//    over chunks): reads q, k, v of each chunk straight from the inputs
+//    (staged through LDS) and the chunk's prep record; wave w owns token tile
+//    w of each chunk and state rows 32w .. 32w+31 of its 16 columns, in
+//    registers in the MFMA accumulator layout.  That layout is also the
+//    B-operand layout of the next products (the reduction index -- state row
+//    or token -- is permuted to match, and the A operands are read in the
+//    same order), so per chunk only the state tiles, (v - ..) and v' (hi/lo
+//    bf16) pass between waves through LDS.
 #include "common.h"
 
 #include <algorithm>
@@ -47,46 +55,29 @@ namespace {
 
 constexpr int kC = 64;
 constexpr int kPitchR = 136;   // bf16 row pitch (272 B) of [64][128] tiles
-constexpr int kPitchT = 72;    // bf16 row pitch (144 B) of transposed tiles
 constexpr int kPitchF = 68;    // fp32 row pitch of [64][64] matrices
 constexpr float kQScale = 0.08838834764831845f;   // 1/sqrt(128)
 
-// Workspace: one record per (chunk, head).  The matrices the scan consumes
-// as MFMA A operands are stored fragment-major (frag_off), so each operand
-// is one contiguous 1 KB wave load.
-constexpr size_t kOffU = 0;                           // fp32 [4 tt][8 cg][64 lane][4]
-constexpr size_t kOffWh = kOffU + 64 * 128 * 4;       // bf16 frag [64][128]
-constexpr size_t kOffWl = kOffWh + 64 * 128 * 2;
-constexpr size_t kOffAh = kOffWl + 64 * 128 * 2;      // bf16 frag [64][64]
-constexpr size_t kOffAl = kOffAh + 64 * 64 * 2;
-constexpr size_t kOffRsq = kOffAl + 64 * 64 * 2;      // fp32 [64]
-constexpr size_t kOffRsk = kOffRsq + 256;             // fp32 [64]
-constexpr size_t kOffEgl = kOffRsk + 256;             // fp32 [1]
-constexpr size_t kOffKt = kOffEgl + 256;              // bf16 frag [128][64] k_raw^T
-constexpr size_t kOffQ = kOffKt + 128 * 64 * 2;       // bf16 frag [64][128] q_raw
-constexpr size_t kUnitBytes = kOffQ + 64 * 128 * 2;
-struct Unit {
-  float* U;
-  bf16* Wh;
-  bf16* Wl;
-  bf16* Ah;
-  bf16* Al;
-  float* rsq;
-  float* rsk;
-  float* egl;
-  bf16* kt;
-  bf16* q;
+// Workspace: one record per (chunk, head): T diag(beta) as hi/lo bf16 A
+// operands, fragment-major (frag_off, two 32-token blocks), the per-token
+// scalars as [kNsc][64] fp32, and Aqk as hi/lo A operands (same layout).
+constexpr size_t kOffTh = 0;
+constexpr size_t kOffTl = kOffTh + 64 * 64 * 2;
+constexpr size_t kOffSc = kOffTl + 64 * 64 * 2;
+enum {
+  kScG = 0,   // G = in-chunk cumsum of g
+  kScKin,     // kinv = 1 / |k|
+  kScQs,      // qinv / sqrt(128)
+  kScCy,      // e^G kinv: row scale of k_raw S
+  kScRsq,     // qinv e^G / sqrt(128): row scale of q_raw S
+  kScRsk,     // kinv e^(G_last - G): row scale of v' in the state update
+  kScEgl,     // [0] = e^(G_last)
+  kNsc
 };
-
-__device__ __forceinline__ Unit unit_at(char* ws, size_t unit) {
-  char* b = ws + unit * kUnitBytes;
-  return Unit{reinterpret_cast<float*>(b + kOffU), reinterpret_cast<bf16*>(b + kOffWh),
-              reinterpret_cast<bf16*>(b + kOffWl), reinterpret_cast<bf16*>(b + kOffAh),
-              reinterpret_cast<bf16*>(b + kOffAl), reinterpret_cast<float*>(b + kOffRsq),
-              reinterpret_cast<float*>(b + kOffRsk), reinterpret_cast<float*>(b + kOffEgl),
-              reinterpret_cast<bf16*>(b + kOffKt),
-              reinterpret_cast<bf16*>(b + kOffQ)};
-}
+constexpr size_t kOffAh = kOffSc + kNsc * 64 * 4;  // bf16 frag [64][64] Aqk hi
+constexpr size_t kOffAl = kOffAh + 64 * 64 * 2;     //                  Aqk lo
+constexpr size_t kUnitBytes = kOffAl + 64 * 64 * 2;
+static_assert(kUnitBytes % 256 == 0, "records stay 256-byte aligned");
 
 __device__ __forceinline__ void split2(float x, bf16& h, bf16& l) {
   h = f2bf(x);
@@ -121,10 +112,8 @@ struct PrepLds {
     bf16 kr[kC * kPitchR];          // k_raw row-major [tok][d]
     float lm[kC * kPitchF];         // L (strictly lower)
   } u;
-  bf16 kt[128 * kPitchT];           // k_raw transposed [d][tok]
-  bf16 vt[128 * kPitchT];           // v transposed [d][tok]
   float tm[kC * kPitchF];           // T; its upper blocks hold scratch products
-  float gs[kC], bs[kC], kinv[kC], qinv[kC], sw[kC];
+  float gs[kC], bs[kC], kinv[kC], qinv[kC];
 };
 
 // C = A B for 16x16 fp32 blocks of [64][kPitchF] matrices (v_mfma 16x16x4).
@@ -138,29 +127,9 @@ __device__ __forceinline__ f32x4 mm16(const float* a, int ar, int ac,
   return acc;
 }
 
-// hi/lo bf16 A operand of row i, columns m0 .. m0+8 of T diag(scale).
-__device__ __forceinline__ void t_operand(const float* tm, const float* scale,
-                                          int i, int m0, bf16x8& hi, bf16x8& lo) {
-  const f32x4 t0 = *reinterpret_cast<const f32x4*>(tm + i * kPitchF + m0);
-  const f32x4 t1 = *reinterpret_cast<const f32x4*>(tm + i * kPitchF + m0 + 4);
-  const f32x4 s0 = *reinterpret_cast<const f32x4*>(scale + m0);
-  const f32x4 s1 = *reinterpret_cast<const f32x4*>(scale + m0 + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    bf16 h, l;
-    split2(t0[e] * s0[e], h, l);
-    hi[e] = h;
-    lo[e] = l;
-    split2(t1[e] * s1[e], h, l);
-    hi[4 + e] = h;
-    lo[4 + e] = l;
-  }
-}
-
 __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k,
-    const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
-    unsigned v_token_stride, const float* __restrict__ g,
+    const bf16* __restrict__ q, const bf16* __restrict__ k, unsigned qk_heads,
+    unsigned qk_token_stride, const float* __restrict__ g,
     const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws, unsigned c0) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PrepLds& s = *reinterpret_cast<PrepLds*>(smem);
@@ -170,27 +139,28 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int li = lane & 15, lg = lane >> 4;
   const unsigned tok0 = c * kC;
-  const Unit un = unit_at(ws, (size_t)c * kGdnHv + h);
+  char* rec = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
+  bf16* th = reinterpret_cast<bf16*>(rec + kOffTh);
+  bf16* tl = reinterpret_cast<bf16*>(rec + kOffTl);
+  float* sc = reinterpret_cast<float*>(rec + kOffSc);
 
-  // S1. rows -> LDS (row-major k; transposed k, v); l2 norms of k and q.
+  // S1. k rows -> LDS; l2 norms of k and q; g, beta.
   {
     const int r = tid >> 2, p = tid & 3;
     const unsigned tok = tok0 + r;
     const bool valid = tok < tokens;
-    bf16x8 k8[4], q8[4], v8[4];
+    bf16x8 k8[4], q8[4];
     if (valid) {
       const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
       const bf16* qp = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
-      const bf16* vp = v + (size_t)tok * v_token_stride + h * kGdnDv + 32 * p;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         k8[i] = ld8(kp + 8 * i);
         q8[i] = ld8(qp + 8 * i);
-        v8[i] = ld8(vp + 8 * i);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) k8[i] = q8[i] = v8[i] = bf16x8{};
+      for (int i = 0; i < 4; ++i) k8[i] = q8[i] = bf16x8{};
     }
     float kss = 0.f, qss = 0.f;
 #pragma unroll
@@ -201,17 +171,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         const float kx = bf2f(k8[i][e]), qx = bf2f(q8[i][e]);
         kss += kx * kx;
         qss += qx * qx;
-        s.kt[(32 * p + 8 * i + e) * kPitchT + r] = k8[i][e];
-        s.vt[(32 * p + 8 * i + e) * kPitchT + r] = v8[i][e];
       }
-    }
-    // q_raw fragments (tile r/16, column block p) for the scan
-#pragma unroll
-    for (int g4 = 0; g4 < 4; ++g4) {
-      const bf16x8 x = q8[g4 >> 1], y = q8[2 + (g4 >> 1)];
-      const int o = 4 * (g4 & 1);
-      *reinterpret_cast<bf16x8*>(un.q + ((((r >> 4) * 4 + p) * 64 + 16 * g4 + (r & 15)) << 3)) =
-          bf16x8{x[o], x[o + 1], x[o + 2], x[o + 3], y[o], y[o + 1], y[o + 2], y[o + 3]};
     }
     kss += __shfl_xor(kss, 1, 64);
     kss += __shfl_xor(kss, 2, 64);
@@ -231,11 +191,11 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
       acc += s.gs[i];
       s.gs[i] = acc;
     }
-    un.egl[0] = expf(acc);
+    sc[kScEgl * 64] = expf(acc);
   }
 
-  // S2. raw k k^T and q k^T on the 10 lower 16x16 tiles (bf16 MFMA: exact
-  // products of the raw inputs); q fragments come straight from global.
+  // S2. raw k k^T and q k^T on the 10 lower 16x16 tiles each (bf16 MFMA:
+  // exact products of the raw inputs); q fragments come straight from global.
   f32x4 acc_job[5];
 #pragma unroll
   for (int jj = 0; jj < 5; ++jj) {
@@ -264,10 +224,16 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
   if (tid < kC) {
     const int r = tid;
     const float eg = expf(s.gs[r]);
-    un.rsq[r] = (s.qinv[r] * kQScale) * eg;
-    un.rsk[r] = s.kinv[r] * expf(s.gs[kC - 1] - s.gs[r]);
-    s.sw[r] = (s.bs[r] * eg) * s.kinv[r];
+    const float qs = s.qinv[r] * kQScale;
+    sc[kScG * 64 + r] = s.gs[r];
+    sc[kScKin * 64 + r] = s.kinv[r];
+    sc[kScQs * 64 + r] = qs;
+    sc[kScCy * 64 + r] = eg * s.kinv[r];
+    sc[kScRsq * 64 + r] = qs * eg;
+    sc[kScRsk * 64 + r] = s.kinv[r] * expf(s.gs[kC - 1] - s.gs[r]);
   }
+  bf16* ah = reinterpret_cast<bf16*>(rec + kOffAh);
+  bf16* al = reinterpret_cast<bf16*>(rec + kOffAl);
 #pragma unroll
   for (int jj = 0; jj < 5; ++jj) {
     const int job = wave + 4 * jj;
@@ -286,14 +252,14 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         const int j = 16 * ct + 4 * lg + r;
         const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
         const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
-        bf16 ah, al;
-        split2(a, ah, al);
-        vh[r] = ah;
-        vl[r] = al;
+        bf16 hh, ll;
+        split2(a, hh, ll);
+        vh[r] = hh;
+        vl[r] = ll;
       }
       const int o = frag_off(i, 16 * ct + 4 * lg, 2);
-      *reinterpret_cast<bf16x4*>(un.Ah + o) = vh;
-      *reinterpret_cast<bf16x4*>(un.Al + o) = vl;
+      *reinterpret_cast<bf16x4*>(ah + o) = vh;
+      *reinterpret_cast<bf16x4*>(al + o) = vl;
     } else {
       const int j = 16 * ct + li;
 #pragma unroll
@@ -305,21 +271,21 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
       }
     }
   }
-  // zero the strictly-upper 16x16 tiles of L and T, and of the stored Aqk
+  for (int idx = tid; idx < 6 * 64; idx += 256) {   // the 6 upper tiles of Aqk
+    const int t = idx >> 6, ln = idx & 63;
+    const int rt = t < 3 ? 0 : (t < 5 ? 1 : 2);
+    const int ct = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
+    const int o = frag_off(16 * rt + (ln & 15), 16 * ct + 4 * (ln >> 4), 2);
+    *reinterpret_cast<bf16x4*>(ah + o) = bf16x4{};
+    *reinterpret_cast<bf16x4*>(al + o) = bf16x4{};
+  }
+  // zero the strictly-upper 16x16 tiles of L and T
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int i = idx >> 6, j = idx & 63;
     if ((j >> 4) > (i >> 4)) {
       s.u.lm[i * kPitchF + j] = 0.f;
       s.tm[i * kPitchF + j] = 0.f;
     }
-  }
-  for (int idx = tid; idx < 6 * 64; idx += 256) {   // 6 upper tiles x 64 lanes
-    const int t = idx >> 6, ln = idx & 63;
-    const int rt = t < 3 ? 0 : (t < 5 ? 1 : 2);
-    const int ct = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    const int o = frag_off(16 * rt + (ln & 15), 16 * ct + 4 * (ln >> 4), 2);
-    *reinterpret_cast<bf16x4*>(un.Ah + o) = bf16x4{};
-    *reinterpret_cast<bf16x4*>(un.Al + o) = bf16x4{};
   }
   __syncthreads();
 
@@ -361,59 +327,23 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     __syncthreads();
   }
 
-  // S5. U = (T diag beta) v, W = (T diag(beta e^G kinv)) k_raw; wave w takes
-  // the 16-column tiles 2w, 2w+1 of both.  The hi/lo A operands are formed
-  // on the fly; T is lower triangular, so the second 32-token step is skipped
-  // for the first two row tiles.
-  const int col0 = 32 * wave + li;   // ct = 2w: col0, ct = 2w+1: col0 + 16
-  for (int rt = 0; rt < 4; ++rt) {
-    f32x4 au[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    f32x4 aw[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    const int nst = rt < 2 ? 1 : 2;
-    for (int st = 0; st < nst; ++st) {
-      bf16x8 tuh, tul, twh, twl;
-      t_operand(s.tm, s.bs, 16 * rt + li, 32 * st + 8 * lg, tuh, tul);
-      t_operand(s.tm, s.sw, 16 * rt + li, 32 * st + 8 * lg, twh, twl);
+  // S5. T diag(beta) as hi/lo A-operand fragments: 4 consecutive columns
+  // are 4 consecutive elements of a fragment.
+  for (int idx = tid; idx < kC * 16; idx += 256) {
+    const int i = idx >> 4, j0 = 4 * (idx & 15);
+    const f32x4 t4 = *reinterpret_cast<const f32x4*>(s.tm + i * kPitchF + j0);
+    const f32x4 b4 = *reinterpret_cast<const f32x4*>(s.bs + j0);
+    bf16x4 hv, lv;
 #pragma unroll
-      for (int ctl = 0; ctl < 2; ++ctl) {
-        const int col = col0 + 16 * ctl;
-        const bf16x8 bv = ld8(s.vt + col * kPitchT + 32 * st + 8 * lg);
-        const bf16x8 bk = ld8(s.kt + col * kPitchT + 32 * st + 8 * lg);
-        au[ctl] = mfma16x16x32(tuh, bv, au[ctl]);
-        au[ctl] = mfma16x16x32(tul, bv, au[ctl]);
-        aw[ctl] = mfma16x16x32(bk, twh, aw[ctl]);   // transposed: W^T
-        aw[ctl] = mfma16x16x32(bk, twl, aw[ctl]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      bf16 hh, ll;
+      split2(t4[e] * b4[e], hh, ll);
+      hv[e] = hh;
+      lv[e] = ll;
     }
-#pragma unroll
-    for (int ctl = 0; ctl < 2; ++ctl) {
-      const int col = col0 + 16 * ctl;
-      reinterpret_cast<f32x4*>(un.U)[(rt * 8 + (col >> 4)) * 64 + 16 * lg + li] = au[ctl];
-    }
-    // aw[ctl][r] = W[16rt + li][32w + 16ctl + 4lg + r]: together the whole
-    // A-operand fragment (row tile rt, column block w) of lane 16lg + li
-    bf16x8 wh, wl;
-#pragma unroll
-    for (int ctl = 0; ctl < 2; ++ctl)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        bf16 h, l;
-        split2(aw[ctl][r], h, l);
-        wh[4 * ctl + r] = h;
-        wl[4 * ctl + r] = l;
-      }
-    const int fo = ((rt * 4 + wave) * 64 + 16 * lg + li) * 8;
-    *reinterpret_cast<bf16x8*>(un.Wh + fo) = wh;
-    *reinterpret_cast<bf16x8*>(un.Wl + fo) = wl;
-  }
-  // k_raw^T (fragment-major) for the scan's state update.
-  for (int idx = tid; idx < 128 * 8; idx += 256) {
-    const int row = idx >> 3, ch = idx & 7, t2 = ch >> 2, g4 = ch & 3;
-    const bf16* src = s.kt + row * kPitchT + 32 * t2 + 4 * g4;
-    const bf16x4 a = *reinterpret_cast<const bf16x4*>(src);
-    const bf16x4 b = *reinterpret_cast<const bf16x4*>(src + 16);
-    *reinterpret_cast<bf16x8*>(un.kt + ((((row >> 4) * 2 + t2) * 64 + 16 * g4 + (row & 15)) << 3)) =
-        bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    const int o = frag_off(i, j0, 2);
+    *reinterpret_cast<bf16x4*>(th + o) = hv;
+    *reinterpret_cast<bf16x4*>(tl + o) = lv;
   }
 }
 
@@ -423,9 +353,18 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 
 constexpr int kScanGroups = kGdnDv / 16;   // 16 v-columns per workgroup
 
+// Scan LDS.  The chain waves' exchange buffers, then the chunk operands the
+// producer waves stage one chunk ahead (by chunk parity): q and k rows
+// (row-major, pitch kPitchR: conflict-free 16-byte row writes and
+// fragment reads; k^T operands come from the same rows through transposed
+// reads) and the record's scalars.
 struct ScanLds {
-  bf16x8 st[8][64];      // [state tile][lane]: S hi (0..3) | lo (4..7)
-  bf16x8 vp[4][64][2];   // [token tile][lane]: {v' hi|lo, rsk v' hi|lo}
+  bf16x8 st[8][64];           // [state tile][lane]: S hi (0..3) | lo (4..7)
+  bf16x8 z[4][64];            // [token tile][lane]: v - cy (k S), hi | lo
+  bf16x8 vp[4][64][2];        // [token tile][lane]: {v' hi|lo, rsk v' hi|lo}
+  bf16 qr[2][kC * kPitchR];
+  bf16 kr[2][kC * kPitchR];
+  float sc[2][kNsc * 64];
 };
 
 __device__ __forceinline__ bf16x8 split4(const f32x4& x) {
@@ -447,146 +386,272 @@ __device__ __forceinline__ void join_pair(const bf16x8& a, const bf16x8& b,
   lo = bf16x8{a[4], a[5], a[6], a[7], b[4], b[5], b[6], b[7]};
 }
 
-// grid = 256 workgroups (32 heads x 8 groups of 16 v-columns; the 8 groups
-// of a head share an XCD, so W/q/Aqk/k^T of a chunk are fetched from HBM once
-// per head).  Wave w owns token tile w of every chunk and state tiles 2w,
-// 2w+1 (rows 32w .. 32w+31), in the MFMA accumulator layout:
-//   sreg[i][r] = S[16(2w+i) + 4lg + r][col].
-// Per chunk: every wave publishes its state tiles (hi/lo) to LDS; computes
-// v' and q S for its 16 tokens and publishes v'; then forms its tokens'
-// outputs and updates its state rows.  Operands come straight from global
-// memory in their stored (pre-permuted) order, one chunk ahead.
-__global__ __launch_bounds__(256, 1) void gdn_chunk_scan_kernel(
-    const char* __restrict__ ws, const float* state_in, float* state_out,
+// A operand of a row-major LDS matrix: row `row`, reduction elements
+// c0 .. c0+3 and c0+16 .. c0+19 (the permuted order of frag_off).
+__device__ __forceinline__ bf16x8 frag_row(const bf16* m, int pitch, int row, int c0) {
+  const bf16x4 a = *reinterpret_cast<const bf16x4*>(m + row * pitch + c0);
+  const bf16x4 b = *reinterpret_cast<const bf16x4*>(m + row * pitch + c0 + 16);
+  return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
+// grid = 256 workgroups of 8 waves (32 heads x 8 groups of 16 v-columns; the
+// 8 groups of a head -- and the two heads of a key head -- share an XCD, so
+// a chunk's q, k and prep record come from HBM once per XCD).
+//  * Chain waves 0-3 (one per SIMD): wave w owns token tile w of every chunk
+//    and state tiles 2w, 2w+1 (rows 32w .. 32w+31), in the MFMA accumulator
+//    layout:  sreg[i][r] = S[16(2w+i) + 4lg + r][col].  Per chunk:
+//      (a) publish the state tiles (hi/lo);
+//      (b) Y = k_raw S and q_raw S for the wave's 16 tokens, publish
+//          Z = v - cy Y;
+//      (c) v' = (T diag beta) Z for the wave's tokens; publish v', rsk v';
+//      (d) o = rsq (q S) + Aqk v', S = e^(G_last) S + k^T (rsk v').
+//  * Producer waves 4-7 (sharing the SIMDs, so their work fills the chain's
+//    stalls): in (a) of chunk c they stage chunk c+1's q rows and scalars
+//    into LDS (the chain reads a chunk's q and scalars in (b) only), in (b)
+//    its k rows (read by the chain up to (d)), and then request chunk c+2's
+//    rows.
+// Each phase ends at a workgroup barrier, and every staged buffer is
+// double-buffered by chunk parity, so a buffer is rewritten only after the
+// barrier that follows its last read.
+__global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
+    const char* __restrict__ ws, const bf16* __restrict__ q, const bf16* __restrict__ k,
+    const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
+    unsigned v_token_stride, const float* state_in, float* state_out,
     bf16* __restrict__ out, unsigned tokens, unsigned c_begin, unsigned c_end) {
-  __shared__ ScanLds s;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  ScanLds& s = *reinterpret_cast<ScanLds*>(smem);
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
   const int h = 4 * xcd + (slot >> 3);
+  const int kh = h * (int)qk_heads / kGdnHv;
   const int cg = slot & 7;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, w = (tid >> 6) & 3, lane = tid & 63;
+  const bool producer = tid >= 256;
   const int li = lane & 15, lg = lane >> 4;
   const int col = 16 * cg + li;
+  const unsigned last = c_end - 1;
 
+  // ---- producer side ------------------------------------------------------
+  // Rows past the last token read as zeros through the buffer ranges (each
+  // range starts at the chunk's first row); loads are unconditional.
+  u32x4 pq[4], pk[4], psc;
+  auto p_fetch = [&](unsigned c) {
+    const unsigned rows = min((unsigned)kC, tokens - c * kC);
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(q) + (size_t)c * kC * qk_token_stride + kh * kGdnDk, 0,
+        (int)(rows * qk_token_stride * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(k) + (size_t)c * kC * qk_token_stride + kh * kGdnDk, 0,
+        (int)(rows * qk_token_stride * 2), 0x00020000);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 16 * w + 4 * u + (lane >> 4);
+      const int off = (int)((row * qk_token_stride + 8 * (lane & 15)) * 2);
+      pq[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, off, 0, 0);
+      pk[u] = __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0);
+    }
+    const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes + kOffSc;
+    const int pt = tid - 256;
+    psc = reinterpret_cast<const u32x4*>(b)[pt < kNsc * 16 ? pt : 0];
+  };
+  // Stage the fetched rows of chunk c (lane: dims 8p .. 8p+7 of row
+  // 16w + 4u + lane/16, p = lane % 16).
+  auto p_stage_k = [&](unsigned c) {
+    const int par = c & 1;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 16 * w + 4 * u + (lane >> 4), d0 = 8 * (lane & 15);
+      *reinterpret_cast<u32x4*>(s.kr[par] + row * kPitchR + d0) = pk[u];
+    }
+  };
+  auto p_stage = [&](unsigned c) {
+    const int par = c & 1;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = 16 * w + 4 * u + (lane >> 4), d0 = 8 * (lane & 15);
+      *reinterpret_cast<u32x4*>(s.qr[par] + row * kPitchR + d0) = pq[u];
+    }
+    const int pt = tid - 256;
+    if (pt < kNsc * 16) reinterpret_cast<u32x4*>(s.sc[par])[pt] = psc;
+  };
+  // ---- chain side -----------------------------------------------------------
   const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
       out, 0, (int)(tokens * kGdnHv * kGdnDv * 2), 0x00020000);
-  f32x4 sreg[2];
   const size_t sb = (size_t)h * kGdnDk * kGdnDv + col;
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
+  f32x4 sreg[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  bf16x8 th[2], tl[2], ah[2], al[2];
+  unsigned vv[4];
+  auto c_fetch_v = [&](unsigned c) {
+    const unsigned rows = min((unsigned)kC, tokens - c * kC);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(v) + (size_t)c * kC * v_token_stride + h * kGdnDv + 16 * cg, 0,
+        (int)(rows * v_token_stride * 2), 0x00020000);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
-
-  struct Stage {
-    bf16x8 wh[4], wl[4], qa[4], ah[2], al[2], kt[2][2];
-    f32x4 u, rsq, rsk;
-    float egl;
+      vv[r] = __builtin_amdgcn_raw_buffer_load_b16(
+          vrs, (int)(((16 * w + 4 * lg + r) * v_token_stride + li) * 2), 0, 0);
   };
-  auto fetch = [&](unsigned c, Stage& st) {
+  auto c_fetch_t = [&](unsigned c) {
     const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
-    const bf16x8* Wh = reinterpret_cast<const bf16x8*>(b + kOffWh) + 256 * w + lane;
-    const bf16x8* Wl = reinterpret_cast<const bf16x8*>(b + kOffWl) + 256 * w + lane;
-    const bf16x8* Q = reinterpret_cast<const bf16x8*>(b + kOffQ) + 256 * w + lane;
+    const bf16x8* Th = reinterpret_cast<const bf16x8*>(b + kOffTh) + 128 * w + lane;
+    const bf16x8* Tl = reinterpret_cast<const bf16x8*>(b + kOffTl) + 128 * w + lane;
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      st.wh[k4] = Wh[64 * k4];
-      st.wl[k4] = Wl[64 * k4];
-      st.qa[k4] = Q[64 * k4];
+    for (int t2 = 0; t2 < 2; ++t2) {
+      th[t2] = Th[64 * t2];
+      tl[t2] = Tl[64 * t2];
     }
+  };
+  auto c_fetch_a = [&](unsigned c) {
+    const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
     const bf16x8* Ah = reinterpret_cast<const bf16x8*>(b + kOffAh) + 128 * w + lane;
     const bf16x8* Al = reinterpret_cast<const bf16x8*>(b + kOffAl) + 128 * w + lane;
-    const bf16x8* Kt = reinterpret_cast<const bf16x8*>(b + kOffKt) + 256 * w + lane;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      st.ah[t2] = Ah[64 * t2];
-      st.al[t2] = Al[64 * t2];
-      st.kt[0][t2] = Kt[64 * t2];
-      st.kt[1][t2] = Kt[128 + 64 * t2];
+      ah[t2] = Ah[64 * t2];
+      al[t2] = Al[64 * t2];
     }
-    st.u = reinterpret_cast<const f32x4*>(b + kOffU)[(8 * w + cg) * 64 + lane];
-    st.rsq = *reinterpret_cast<const f32x4*>(b + kOffRsq + 4 * (16 * w + 4 * lg));
-    st.rsk = *reinterpret_cast<const f32x4*>(b + kOffRsk + 4 * (16 * w + 4 * lg));
-    st.egl = *reinterpret_cast<const float*>(b + kOffEgl);
   };
 
-  auto step = [&](const Stage& st, unsigned c) {
-    // publish this wave's state tiles
+  // ---- prologue -------------------------------------------------------------
+  if (producer) {
+    p_fetch(c_begin);
+    p_stage(c_begin);
+    p_stage_k(c_begin);
+    p_fetch(c_begin + 1 < last ? c_begin + 1 : last);
+  } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) s.st[2 * w + i][lane] = split4(sreg[i]);
-    lds_barrier();
-    // v' = U - W S and q_raw S for token tile w (reduction over 128 rows)
-    f32x4 aw = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      bf16x8 shi, slo;
-      join_pair(s.st[2 * k4][lane], s.st[2 * k4 + 1][lane], shi, slo);
-      aw = mfma16x16x32(st.wh[k4], shi, aw);
-      aq = mfma16x16x32(st.qa[k4], shi, aq);
-      aw = mfma16x16x32(st.wh[k4], slo, aw);
-      aq = mfma16x16x32(st.qa[k4], slo, aq);
-      aw = mfma16x16x32(st.wl[k4], shi, aw);
-    }
-    const f32x4 vp = st.u - aw;
-    const f32x4 vz = st.rsk * vp;
-    s.vp[w][lane][0] = split4(vp);
-    s.vp[w][lane][1] = split4(vz);
-    f32x4 acc = st.rsq * aq;
-    lds_barrier();
-    // o = rsq (q_raw S) + Aqk v'  (Aqk is lower triangular: tiles 0, 1 only
-    // need the first 32 tokens)
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      if (t2 == 1 && w < 2) break;
-      bf16x8 vh, vl;
-      join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
-      acc = mfma16x16x32(st.ah[t2], vh, acc);
-      acc = mfma16x16x32(st.ah[t2], vl, acc);
-      acc = mfma16x16x32(st.al[t2], vh, acc);
-    }
-    // S = exp(G_last) S + k_raw^T (rsk v')
-    f32x4 sn[2] = {sreg[0] * st.egl, sreg[1] * st.egl};
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      bf16x8 zh, zl;
-      join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        sn[i] = mfma16x16x32(st.kt[i][t2], zh, sn[i]);
-        sn[i] = mfma16x16x32(st.kt[i][t2], zl, sn[i]);
-      }
-    }
-    sreg[0] = sn[0];
-    sreg[1] = sn[1];
-    // Output rows past the end fall outside the buffer range and are dropped
-    // by the hardware (no branch, so no uncertain store count).
-    const unsigned tb = c * kC + 16 * w + 4 * lg;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_buffer_store_b16(
-          __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
-          (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
-  };
-
-  // Two operand stages alternate (loop unrolled by two): chunk c+1's loads
-  // are in flight while chunk c is computed.
-  // Two operand stages alternate (loop unrolled by two): chunk c+1's loads
-  // are in flight while chunk c is computed.  Fetches past the last chunk
-  // re-read it, keeping every fetch unconditional.
-  Stage s0, s1;
-  const unsigned last = c_end - 1;
-  fetch(c_begin, s0);
-  for (unsigned c = c_begin; c < c_end; c += 2) {
-    fetch(c + 1 < last ? c + 1 : last, s1);
-    step(s0, c);
-    if (c + 1 >= c_end) break;
-    fetch(c + 2 < last ? c + 2 : last, s0);
-    step(s1, c + 1);
+      for (int r = 0; r < 4; ++r)
+        sreg[i][r] =
+            state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
+    c_fetch_v(c_begin);
+    c_fetch_t(c_begin);
+    c_fetch_a(c_begin);
   }
+  lds_barrier();
+
+  for (unsigned c = c_begin; c < c_end; ++c) {
+    const int par = c & 1;
+    const unsigned nxt = c + 1 < last ? c + 1 : last;
+    // (a)
+    if (producer) {
+      if (c + 1 < c_end) p_stage(c + 1);
+    } else {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i) s.st[2 * w + i][lane] = split4(sreg[i]);
+    }
+    lds_barrier();
+    // (b)
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, rsk;
+    float egl;
+    if (producer) {
+      if (c + 1 < c_end) p_stage_k(c + 1);
+      p_fetch(c + 2 < last ? c + 2 : last);
+    } else {
+      const float* sc = s.sc[par];
+      // four independent accumulator chains (hi and lo halves of S)
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      f32x4 ay = zero, aqs = zero, ay2 = zero, aqs2 = zero;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
+      for (int k4 = 0; k4 < 4; ++k4) {
+        bf16x8 shi, slo;
+        join_pair(s.st[2 * k4][lane], s.st[2 * k4 + 1][lane], shi, slo);
+        const bf16x8 kfa = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+        const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+        ay = mfma16x16x32(kfa, shi, ay);
+        aqs = mfma16x16x32(qfa, shi, aqs);
+        ay2 = mfma16x16x32(kfa, slo, ay2);
+        aqs2 = mfma16x16x32(qfa, slo, aqs2);
+      }
+      ay += ay2;
+      aqs += aqs2;
+      const int r0 = 16 * w + 4 * lg;
+      const f32x4 cy = *reinterpret_cast<const f32x4*>(sc + kScCy * 64 + r0);
+      const f32x4 rsq = *reinterpret_cast<const f32x4*>(sc + kScRsq * 64 + r0);
+      rsk = *reinterpret_cast<const f32x4*>(sc + kScRsk * 64 + r0);
+      egl = sc[kScEgl * 64];
+      f32x4 zv;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
+      s.z[w][lane] = split4(zv);
+      acc = rsq * aqs;
+      c_fetch_v(nxt);
+    }
+    lds_barrier();
+    // (c) v' = (T diag beta) Z: T is lower triangular, so token tiles 0, 1
+    // only reduce over the first 32 tokens
+    if (!producer) {
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      f32x4 vp = zero, vp2 = zero, vp3 = zero;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        if (t2 == 1 && w < 2) break;
+        bf16x8 zh, zl;
+        join_pair(s.z[2 * t2][lane], s.z[2 * t2 + 1][lane], zh, zl);
+        vp = mfma16x16x32(th[t2], zh, vp);
+        vp2 = mfma16x16x32(th[t2], zl, vp2);
+        vp3 = mfma16x16x32(tl[t2], zh, vp3);
+      }
+      vp += vp2 + vp3;
+      s.vp[w][lane][0] = split4(vp);
+      s.vp[w][lane][1] = split4(rsk * vp);
+      c_fetch_t(nxt);
+    }
+    lds_barrier();
+    // (d)
+    if (!producer) {
+      // o = rsq (q_raw S) + Aqk v'
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc2 = zero, acc3 = zero;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        if (t2 == 1 && w < 2) break;
+        bf16x8 vh, vl;
+        join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
+        acc = mfma16x16x32(ah[t2], vh, acc);
+        acc2 = mfma16x16x32(ah[t2], vl, acc2);
+        acc3 = mfma16x16x32(al[t2], vh, acc3);
+      }
+      acc += acc2 + acc3;
+      // S = exp(G_last) S + k_raw^T (rsk v')
+      f32x4 sn[2] = {sreg[0] * egl, sreg[1] * egl};
+      f32x4 sl[2] = {zero, zero};
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        bf16x8 zh, zl;
+        join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          // k^T A operand (row = dim 16(2w+i) + li, reduction = tokens
+          // 32t2 + 4lg + e and +16) by transposed reads of the k rows
+          const bf16* ra = s.kr[par] + (32 * t2 + 4 * lg + (li >> 2)) * kPitchR +
+                           16 * (2 * w + i) + 4 * (li & 3);
+          const bf16x8 ktf = cat_bf16x8(lds_read_tr16(ra), lds_read_tr16(ra + 16 * kPitchR));
+          sn[i] = mfma16x16x32(ktf, zh, sn[i]);
+          sl[i] = mfma16x16x32(ktf, zl, sl[i]);
+        }
+      }
+      sreg[0] = sn[0] + sl[0];
+      sreg[1] = sn[1] + sl[1];
+      c_fetch_a(nxt);
+      // Output rows past the end fall outside the buffer range and are
+      // dropped by the hardware (no branch, so no uncertain store count).
+      const unsigned tb = c * kC + 16 * w + 4 * lg;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
+            (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
+    }
+  }
+  if (!producer) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
+  }
 }
 
 // Prep / scan overlap: a second stream and events per device, created on
@@ -648,6 +713,10 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
     attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_chunk_prep_kernel),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (int)sizeof(PrepLds));
+    if (attr_status == hipSuccess)
+      attr_status = hipFuncSetAttribute(reinterpret_cast<const void*>(gdn_chunk_scan_kernel),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        (int)sizeof(ScanLds));
   });
   if (attr_status != hipSuccess) return (int)attr_status;
   char* wsb = static_cast<char*>(workspace);
@@ -659,12 +728,13 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   float* so = static_cast<float*>(state_out);
   auto prep = [&](unsigned c0, unsigned c1, hipStream_t s) {
     hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(c1 - c0, kGdnHv), dim3(256),
-                       sizeof(PrepLds), s, qb, kb, vb, qk_heads, qk_token_stride,
-                       v_token_stride, gb, bb, tokens, wsb, c0);
+                       sizeof(PrepLds), s, qb, kb, qk_heads, qk_token_stride, gb, bb, tokens,
+                       wsb, c0);
   };
   auto scan = [&](unsigned c0, unsigned c1, const float* sin) {
-    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(256), 0, st,
-                       wsb, sin, so, static_cast<bf16*>(out), tokens, c0, c1);
+    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(512),
+                       sizeof(ScanLds), st, wsb, qb, kb, vb, qk_heads, qk_token_stride,
+                       v_token_stride, sin, so, static_cast<bf16*>(out), tokens, c0, c1);
   };
   const unsigned ranges = std::min(kMaxRanges, n_chunks / kMinRangeChunks);
   if (ranges < 2) {
