@@ -47,7 +47,6 @@
 //    bf16) pass between waves through LDS.
 #include "common.h"
 
-#include <algorithm>
 #include <mutex>
 
 namespace q36 {
@@ -359,7 +358,7 @@ constexpr int kScanGroups = kGdnDv / 16;   // 16 v-columns per workgroup
 // fragment reads; k^T operands come from the same rows through transposed
 // reads) and the record's scalars.
 struct ScanLds {
-  bf16x8 st[8][64];           // [state tile][lane]: S hi (0..3) | lo (4..7)
+  bf16x8 st[4][2][64];        // [state tile pair][hi, lo][lane]: B operands
   bf16x8 z[4][64];            // [token tile][lane]: v - cy (k S), hi | lo
   bf16x8 vp[4][64][2];        // [token tile][lane]: {v' hi|lo, rsk v' hi|lo}
   bf16 qr[2][kC * kPitchR];
@@ -511,78 +510,83 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
   };
 
-  // ---- prologue -------------------------------------------------------------
+  // The two roles run separate loops (straight-line code per role, so the
+  // compiler's in-order wait counts follow each role's own loads) with the
+  // same barrier sequence: one after the prologue, three per chunk.
   if (producer) {
     p_fetch(c_begin);
     p_stage(c_begin);
     p_stage_k(c_begin);
     p_fetch(c_begin + 1 < last ? c_begin + 1 : last);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sreg[i][r] =
-            state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
-    c_fetch_v(c_begin);
-    c_fetch_t(c_begin);
-    c_fetch_a(c_begin);
+    lds_barrier();
+    for (unsigned c = c_begin; c < c_end; ++c) {
+      // (a) chunk c+1's q rows and scalars (last read by the chain in (b)
+      // of chunk c-1)
+      if (c + 1 < c_end) p_stage(c + 1);
+      lds_barrier();
+      // (b) chunk c+1's k rows (last read by the chain in (d) of chunk
+      // c-1), then request chunk c+2's rows
+      if (c + 1 < c_end) p_stage_k(c + 1);
+      p_fetch(c + 2 < last ? c + 2 : last);
+      lds_barrier();
+      lds_barrier();
+    }
+    return;
   }
-  lds_barrier();
 
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
+  c_fetch_v(c_begin);
+  c_fetch_t(c_begin);
+  c_fetch_a(c_begin);
+  lds_barrier();
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   for (unsigned c = c_begin; c < c_end; ++c) {
     const int par = c & 1;
     const unsigned nxt = c + 1 < last ? c + 1 : last;
-    // (a)
-    if (producer) {
-      if (c + 1 < c_end) p_stage(c + 1);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) s.st[2 * w + i][lane] = split4(sreg[i]);
+    // (a) publish the state tiles as the hi / lo B operands of tile pair w
+    {
+      bf16x8 hi, lo;
+      join_pair(split4(sreg[0]), split4(sreg[1]), hi, lo);
+      s.st[w][0][lane] = hi;
+      s.st[w][1][lane] = lo;
     }
     lds_barrier();
-    // (b)
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f}, rsk;
-    float egl;
-    if (producer) {
-      if (c + 1 < c_end) p_stage_k(c + 1);
-      p_fetch(c + 2 < last ? c + 2 : last);
-    } else {
-      const float* sc = s.sc[par];
-      // four independent accumulator chains (hi and lo halves of S)
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      f32x4 ay = zero, aqs = zero, ay2 = zero, aqs2 = zero;
+    // (b) Y = k_raw S, q_raw S (four independent accumulator chains: the hi
+    // and lo halves of S), Z = v - cy Y
+    const float* sc = s.sc[par];
+    f32x4 ay = zero, aqs = zero, ay2 = zero, aqs2 = zero;
 #pragma unroll
-      for (int k4 = 0; k4 < 4; ++k4) {
-        bf16x8 shi, slo;
-        join_pair(s.st[2 * k4][lane], s.st[2 * k4 + 1][lane], shi, slo);
-        const bf16x8 kfa = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-        const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-        ay = mfma16x16x32(kfa, shi, ay);
-        aqs = mfma16x16x32(qfa, shi, aqs);
-        ay2 = mfma16x16x32(kfa, slo, ay2);
-        aqs2 = mfma16x16x32(qfa, slo, aqs2);
-      }
-      ay += ay2;
-      aqs += aqs2;
-      const int r0 = 16 * w + 4 * lg;
-      const f32x4 cy = *reinterpret_cast<const f32x4*>(sc + kScCy * 64 + r0);
-      const f32x4 rsq = *reinterpret_cast<const f32x4*>(sc + kScRsq * 64 + r0);
-      rsk = *reinterpret_cast<const f32x4*>(sc + kScRsk * 64 + r0);
-      egl = sc[kScEgl * 64];
-      f32x4 zv;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
-      s.z[w][lane] = split4(zv);
-      acc = rsq * aqs;
-      c_fetch_v(nxt);
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const bf16x8 shi = s.st[k4][0][lane], slo = s.st[k4][1][lane];
+      const bf16x8 kfa = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+      const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+      ay = mfma16x16x32(kfa, shi, ay);
+      aqs = mfma16x16x32(qfa, shi, aqs);
+      ay2 = mfma16x16x32(kfa, slo, ay2);
+      aqs2 = mfma16x16x32(qfa, slo, aqs2);
     }
+    ay += ay2;
+    aqs += aqs2;
+    const int r0 = 16 * w + 4 * lg;
+    const f32x4 cy = *reinterpret_cast<const f32x4*>(sc + kScCy * 64 + r0);
+    const f32x4 rsq = *reinterpret_cast<const f32x4*>(sc + kScRsq * 64 + r0);
+    const f32x4 rsk = *reinterpret_cast<const f32x4*>(sc + kScRsk * 64 + r0);
+    const float egl = sc[kScEgl * 64];
+    f32x4 zv;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
+    s.z[w][lane] = split4(zv);
+    f32x4 acc = rsq * aqs;
+    c_fetch_v(nxt);
     lds_barrier();
     // (c) v' = (T diag beta) Z: T is lower triangular, so token tiles 0, 1
     // only reduce over the first 32 tokens
-    if (!producer) {
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    {
       f32x4 vp = zero, vp2 = zero, vp3 = zero;
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
@@ -596,89 +600,56 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
       vp += vp2 + vp3;
       s.vp[w][lane][0] = split4(vp);
       s.vp[w][lane][1] = split4(rsk * vp);
-      c_fetch_t(nxt);
     }
+    c_fetch_t(nxt);
     lds_barrier();
-    // (d)
-    if (!producer) {
-      // o = rsq (q_raw S) + Aqk v'
-      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-      f32x4 acc2 = zero, acc3 = zero;
+    // (d) o = rsq (q_raw S) + Aqk v'
+    f32x4 acc2 = zero, acc3 = zero;
 #pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        if (t2 == 1 && w < 2) break;
-        bf16x8 vh, vl;
-        join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
-        acc = mfma16x16x32(ah[t2], vh, acc);
-        acc2 = mfma16x16x32(ah[t2], vl, acc2);
-        acc3 = mfma16x16x32(al[t2], vh, acc3);
-      }
-      acc += acc2 + acc3;
-      // S = exp(G_last) S + k_raw^T (rsk v')
-      f32x4 sn[2] = {sreg[0] * egl, sreg[1] * egl};
-      f32x4 sl[2] = {zero, zero};
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        bf16x8 zh, zl;
-        join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          // k^T A operand (row = dim 16(2w+i) + li, reduction = tokens
-          // 32t2 + 4lg + e and +16) by transposed reads of the k rows
-          const bf16* ra = s.kr[par] + (32 * t2 + 4 * lg + (li >> 2)) * kPitchR +
-                           16 * (2 * w + i) + 4 * (li & 3);
-          const bf16x8 ktf = cat_bf16x8(lds_read_tr16(ra), lds_read_tr16(ra + 16 * kPitchR));
-          sn[i] = mfma16x16x32(ktf, zh, sn[i]);
-          sl[i] = mfma16x16x32(ktf, zl, sl[i]);
-        }
-      }
-      sreg[0] = sn[0] + sl[0];
-      sreg[1] = sn[1] + sl[1];
-      c_fetch_a(nxt);
-      // Output rows past the end fall outside the buffer range and are
-      // dropped by the hardware (no branch, so no uncertain store count).
-      const unsigned tb = c * kC + 16 * w + 4 * lg;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        __builtin_amdgcn_raw_buffer_store_b16(
-            __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
-            (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
+    for (int t2 = 0; t2 < 2; ++t2) {
+      if (t2 == 1 && w < 2) break;
+      bf16x8 vh, vl;
+      join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
+      acc = mfma16x16x32(ah[t2], vh, acc);
+      acc2 = mfma16x16x32(ah[t2], vl, acc2);
+      acc3 = mfma16x16x32(al[t2], vh, acc3);
     }
-  }
-  if (!producer) {
+    acc += acc2 + acc3;
+    // S = exp(G_last) S + k_raw^T (rsk v')
+    f32x4 sn[2] = {sreg[0] * egl, sreg[1] * egl};
+    f32x4 sl[2] = {zero, zero};
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int t2 = 0; t2 < 2; ++t2) {
+      bf16x8 zh, zl;
+      join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
+      for (int i = 0; i < 2; ++i) {
+        // k^T A operand (row = dim 16(2w+i) + li, reduction = tokens
+        // 32t2 + 4lg + e and +16) by transposed reads of the k rows
+        const bf16* ra = s.kr[par] + (32 * t2 + 4 * lg + (li >> 2)) * kPitchR +
+                         16 * (2 * w + i) + 4 * (li & 3);
+        const bf16x8 ktf = cat_bf16x8(lds_read_tr16(ra), lds_read_tr16(ra + 16 * kPitchR));
+        sn[i] = mfma16x16x32(ktf, zh, sn[i]);
+        sl[i] = mfma16x16x32(ktf, zl, sl[i]);
+      }
+    }
+    sreg[0] = sn[0] + sl[0];
+    sreg[1] = sn[1] + sl[1];
+    c_fetch_a(nxt);
+    // Output rows past the end fall outside the buffer range and are
+    // dropped by the hardware (no branch, so no uncertain store count).
+    const unsigned tb = c * kC + 16 * w + 4 * lg;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_buffer_store_b16(
+          __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
+          (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
   }
-}
-
-// Prep / scan overlap: a second stream and events per device, created on
-// first use and kept for the life of the process.
-constexpr unsigned kMaxRanges = 8;        // chunk ranges per call
-constexpr unsigned kMinRangeChunks = 16;  // below 2 x 16 chunks: one prep + one scan
-struct Overlap {
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr;
-  hipEvent_t done[kMaxRanges] = {};
-};
-std::mutex g_overlap_mutex;     // one enqueue sequence at a time (shared events)
-Overlap g_overlap[64];
-bool g_overlap_ready[64] = {};
-
-Overlap* overlap_for_current_device() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  Overlap& o = g_overlap[dev];
-  if (!g_overlap_ready[dev]) {
-    if (hipStreamCreateWithFlags(&o.side, hipStreamNonBlocking) != hipSuccess) return nullptr;
-    if (hipEventCreateWithFlags(&o.fork, hipEventDisableTiming) != hipSuccess) return nullptr;
-    for (auto& ev : o.done)
-      if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) return nullptr;
-    g_overlap_ready[dev] = true;
-  }
-  return &o;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
 }
 
 }  // namespace
@@ -726,44 +697,13 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   const float* gb = static_cast<const float*>(g);
   const float* bb = static_cast<const float*>(beta);
   float* so = static_cast<float*>(state_out);
-  auto prep = [&](unsigned c0, unsigned c1, hipStream_t s) {
-    hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(c1 - c0, kGdnHv), dim3(256),
-                       sizeof(PrepLds), s, qb, kb, qk_heads, qk_token_stride, gb, bb, tokens,
-                       wsb, c0);
-  };
-  auto scan = [&](unsigned c0, unsigned c1, const float* sin) {
-    hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(512),
-                       sizeof(ScanLds), st, wsb, qb, kb, vb, qk_heads, qk_token_stride,
-                       v_token_stride, sin, so, static_cast<bf16*>(out), tokens, c0, c1);
-  };
-  const unsigned ranges = std::min(kMaxRanges, n_chunks / kMinRangeChunks);
-  if (ranges < 2) {
-    prep(0, n_chunks, st);
-    scan(0, n_chunks, static_cast<const float*>(state_in));
-    return static_cast<int>(hipGetLastError());
-  }
-  // Prep of chunk range r + 1 overlaps the scan of range r: prep ranges run
-  // in order on a second stream, each scan range waits for its prep range's
-  // event; the state is carried through state_out.
-  std::lock_guard<std::mutex> lock(g_overlap_mutex);
-  Overlap* ov = overlap_for_current_device();
-  if (ov == nullptr) return Q36_EINVAL;
-  hipError_t e = hipEventRecord(ov->fork, st);
-  if (e == hipSuccess) e = hipStreamWaitEvent(ov->side, ov->fork, 0);
-  if (e != hipSuccess) return (int)e;
-  for (unsigned r = 0; r < ranges; ++r) {
-    const unsigned c0 = (unsigned)((uint64_t)n_chunks * r / ranges);
-    const unsigned c1 = (unsigned)((uint64_t)n_chunks * (r + 1) / ranges);
-    prep(c0, c1, ov->side);
-    e = hipEventRecord(ov->done[r], ov->side);
-    if (e != hipSuccess) return (int)e;
-  }
-  for (unsigned r = 0; r < ranges; ++r) {
-    const unsigned c0 = (unsigned)((uint64_t)n_chunks * r / ranges);
-    const unsigned c1 = (unsigned)((uint64_t)n_chunks * (r + 1) / ranges);
-    e = hipStreamWaitEvent(st, ov->done[r], 0);
-    if (e != hipSuccess) return (int)e;
-    scan(c0, c1, r == 0 ? static_cast<const float*>(state_in) : so);
-  }
+  // Prep over every chunk, then the scan: the scan's workgroups take a whole
+  // CU's LDS, so a concurrent prep would only delay them.
+  hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256), sizeof(PrepLds), st,
+                     qb, kb, qk_heads, qk_token_stride, gb, bb, tokens, wsb, 0u);
+  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(512),
+                     sizeof(ScanLds), st, wsb, qb, kb, vb, qk_heads, qk_token_stride,
+                     v_token_stride, static_cast<const float*>(state_in), so,
+                     static_cast<bf16*>(out), tokens, 0u, n_chunks);
   return static_cast<int>(hipGetLastError());
 }
