@@ -359,23 +359,49 @@ constexpr int kScanGroups = kGdnDv / 16;   // 16 v-columns per workgroup
 // reads) and the record's scalars.
 struct ScanLds {
   bf16x8 st[4][2][64];        // [state tile pair][hi, lo][lane]: B operands
-  bf16x8 z[4][64];            // [token tile][lane]: v - cy (k S), hi | lo
-  bf16x8 vp[4][64][2];        // [token tile][lane]: {v' hi|lo, rsk v' hi|lo}
+  // Exchanged token tiles as ready B operands: [32-token block][hi, lo]
+  // [lane]; token tile t fills elements 4 (t % 2) .. +3 of block t / 2.
+  bf16x8 z[2][2][64];         // v - cy (k S)
+  bf16x8 vp[2][2][2][64];     // [v', rsk v'][block][hi, lo][lane]
   bf16 qr[2][kC * kPitchR];
   bf16 kr[2][kC * kPitchR];
   float sc[2][kNsc * 64];
 };
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// split2 on a pair, converting two values per instruction: hi = bf16(x),
+// lo = bf16(x - hi), with hi widened back by shifting / masking the pair.
+__device__ __forceinline__ void split_pair(float x0, float x1, bf16x2& hi, bf16x2& lo) {
+  hi = __builtin_convertvector(f32x2{x0, x1}, bf16x2);
+  const unsigned u = __builtin_bit_cast(unsigned, hi);
+  const float h0 = __builtin_bit_cast(float, u << 16);
+  const float h1 = __builtin_bit_cast(float, u & 0xffff0000u);
+  lo = __builtin_convertvector(f32x2{x0 - h0, x1 - h1}, bf16x2);
+}
+
+__device__ __forceinline__ void split4x(const f32x4& x, bf16x4& hi, bf16x4& lo) {
+  bf16x2 h01, l01, h23, l23;
+  split_pair(x[0], x[1], h01, l01);
+  split_pair(x[2], x[3], h23, l23);
+  hi = bf16x4{h01[0], h01[1], h23[0], h23[1]};
+  lo = bf16x4{l01[0], l01[1], l23[0], l23[1]};
+}
+
 __device__ __forceinline__ bf16x8 split4(const f32x4& x) {
-  bf16x8 out;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    bf16 h, l;
-    split2(x[e], h, l);
-    out[e] = h;
-    out[4 + e] = l;
-  }
-  return out;
+  bf16x4 hi, lo;
+  split4x(x, hi, lo);
+  return bf16x8{hi[0], hi[1], hi[2], hi[3], lo[0], lo[1], lo[2], lo[3]};
+}
+
+// Publish token tile t of an exchanged pair of B operands (see ScanLds).
+__device__ __forceinline__ void put_tile(bf16x8 (&blk)[2][2][64], int t, int lane,
+                                         const f32x4& x) {
+  bf16x4 hi, lo;
+  split4x(x, hi, lo);
+  *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(&blk[t >> 1][0][lane]) + 4 * (t & 1)) = hi;
+  *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(&blk[t >> 1][1][lane]) + 4 * (t & 1)) = lo;
 }
 
 // B operands (hi, lo) from two published accumulator tiles.
@@ -580,7 +606,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
-    s.z[w][lane] = split4(zv);
+    put_tile(s.z, w, lane, zv);
     f32x4 acc = rsq * aqs;
     c_fetch_v(nxt);
     lds_barrier();
@@ -591,15 +617,14 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         if (t2 == 1 && w < 2) break;
-        bf16x8 zh, zl;
-        join_pair(s.z[2 * t2][lane], s.z[2 * t2 + 1][lane], zh, zl);
+        const bf16x8 zh = s.z[t2][0][lane], zl = s.z[t2][1][lane];
         vp = mfma16x16x32(th[t2], zh, vp);
         vp2 = mfma16x16x32(th[t2], zl, vp2);
         vp3 = mfma16x16x32(tl[t2], zh, vp3);
       }
       vp += vp2 + vp3;
-      s.vp[w][lane][0] = split4(vp);
-      s.vp[w][lane][1] = split4(rsk * vp);
+      put_tile(s.vp[0], w, lane, vp);
+      put_tile(s.vp[1], w, lane, rsk * vp);
     }
     c_fetch_t(nxt);
     lds_barrier();
@@ -608,8 +633,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       if (t2 == 1 && w < 2) break;
-      bf16x8 vh, vl;
-      join_pair(s.vp[2 * t2][lane][0], s.vp[2 * t2 + 1][lane][0], vh, vl);
+      const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
       acc = mfma16x16x32(ah[t2], vh, acc);
       acc2 = mfma16x16x32(ah[t2], vl, acc2);
       acc3 = mfma16x16x32(al[t2], vh, acc3);
@@ -620,8 +644,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     f32x4 sl[2] = {zero, zero};
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      bf16x8 zh, zl;
-      join_pair(s.vp[2 * t2][lane][1], s.vp[2 * t2 + 1][lane][1], zh, zl);
+      const bf16x8 zh = s.vp[1][t2][0][lane], zl = s.vp[1][t2][1][lane];
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         // k^T A operand (row = dim 16(2w+i) + li, reduction = tokens
