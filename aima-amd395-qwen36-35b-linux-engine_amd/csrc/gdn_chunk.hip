@@ -126,6 +126,14 @@ __device__ __forceinline__ f32x4 mm16(const float* a, int ar, int ac,
   return acc;
 }
 
+// Lower-triangular 16x16 tile t (0..9) of a 64x64 matrix, row-major over
+// the tiles: row tile rt, column tile ct <= rt.
+__device__ __forceinline__ int tri_row(int t) { return (t >= 1) + (t >= 3) + (t >= 6); }
+__device__ __forceinline__ int tri_col(int t) {
+  const int rt = tri_row(t);
+  return t - rt * (rt + 1) / 2;
+}
+
 __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, unsigned qk_heads,
     unsigned qk_token_stride, const float* __restrict__ g,
@@ -143,23 +151,43 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
   bf16* tl = reinterpret_cast<bf16*>(rec + kOffTl);
   float* sc = reinterpret_cast<float*>(rec + kOffSc);
 
+  // Every input load is unconditional and issued up front (one memory
+  // round trip): rows past the last token read as zeros through the buffer
+  // ranges, g and beta are read at a clamped row and zeroed.
+  const unsigned rows = min((unsigned)kC, tokens - tok0);
+  const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(q) + (size_t)tok0 * qk_token_stride + kh * kGdnDk, 0,
+      (int)(rows * qk_token_stride * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(k) + (size_t)tok0 * qk_token_stride + kh * kGdnDk, 0,
+      (int)(rows * qk_token_stride * 2), 0x00020000);
+  auto ldq = [&](const __amdgpu_buffer_rsrc_t& rs, int row, int col) {
+    return __builtin_bit_cast(
+        bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((row * qk_token_stride + col) * 2), 0, 0));
+  };
+  // q fragments of this wave's q k^T jobs (jobs 10..19: jj = 2 for waves 2
+  // and 3, jj = 3, 4 for every wave)
+  bf16x8 qpre[3][4];
+#pragma unroll
+  for (int jq = 0; jq < 3; ++jq) {
+    const int job = wave + 4 * (jq + 2);
+    const int rt = tri_row(job >= 10 ? job - 10 : 0);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qpre[jq][st] = ldq(qrs, 16 * rt + li, 8 * lg + 32 * st);
+  }
+
   // S1. k rows -> LDS; l2 norms of k and q; g, beta.
   {
     const int r = tid >> 2, p = tid & 3;
     const unsigned tok = tok0 + r;
     const bool valid = tok < tokens;
+    const unsigned tcl = valid ? tok : tokens - 1;
+    const float gval = g[(size_t)tcl * kGdnHv + h], bval = beta[(size_t)tcl * kGdnHv + h];
     bf16x8 k8[4], q8[4];
-    if (valid) {
-      const bf16* kp = k + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
-      const bf16* qp = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 32 * p;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        k8[i] = ld8(kp + 8 * i);
-        q8[i] = ld8(qp + 8 * i);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) k8[i] = q8[i] = bf16x8{};
+    for (int i = 0; i < 4; ++i) {
+      k8[i] = ldq(krs, r, 32 * p + 8 * i);
+      q8[i] = ldq(qrs, r, 32 * p + 8 * i);
     }
     float kss = 0.f, qss = 0.f;
 #pragma unroll
@@ -179,17 +207,25 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     if (p == 0) {
       s.kinv[r] = rsqrt_rn(kss + 1e-6f);
       s.qinv[r] = rsqrt_rn(qss + 1e-6f);
-      s.gs[r] = valid ? g[(size_t)tok * kGdnHv + h] : 0.f;
-      s.bs[r] = valid ? beta[(size_t)tok * kGdnHv + h] : 0.f;
+      s.gs[r] = valid ? gval : 0.f;
+      s.bs[r] = valid ? bval : 0.f;
     }
   }
-  __syncthreads();
-  if (tid == 0) {  // sequential fp32 cumsum, as torch.cumsum
+  lds_barrier();
+  if (tid == 0) {  // sequential fp32 cumsum, as torch.cumsum (in registers)
+    f32x4 gv[kC / 4];
+#pragma unroll
+    for (int i = 0; i < kC / 4; ++i) gv[i] = reinterpret_cast<const f32x4*>(s.gs)[i];
     float acc = 0.f;
-    for (int i = 0; i < kC; ++i) {
-      acc += s.gs[i];
-      s.gs[i] = acc;
-    }
+#pragma unroll
+    for (int i = 0; i < kC / 4; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        acc += gv[i][e];
+        gv[i][e] = acc;
+      }
+#pragma unroll
+    for (int i = 0; i < kC / 4; ++i) reinterpret_cast<f32x4*>(s.gs)[i] = gv[i];
     sc[kScEgl * 64] = expf(acc);
   }
 
@@ -200,18 +236,14 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
   for (int jj = 0; jj < 5; ++jj) {
     const int job = wave + 4 * jj;
     const bool is_q = job >= 10;
-    int t = is_q ? job - 10 : job;
-    int rt = 0;
-    while (t > rt) { t -= rt + 1; ++rt; }
-    const int ct = t;
+    const int t = is_q ? job - 10 : job;
+    const int rt = tri_row(t), ct = tri_col(t);
     const bf16* brow = s.u.kr + (16 * ct + li) * kPitchR + 8 * lg;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     if (is_q) {
-      const unsigned tok = tok0 + 16 * rt + li;
-      const bf16* qrow = q + (size_t)tok * qk_token_stride + kh * kGdnDk + 8 * lg;
 #pragma unroll
       for (int st = 0; st < 4; ++st)   // transposed: D[j][i] = k_j . q_i
-        acc = mfma16x16x32(ld8(brow + 32 * st), tok < tokens ? ld8(qrow + 32 * st) : bf16x8{}, acc);
+        acc = mfma16x16x32(ld8(brow + 32 * st), qpre[jj >= 2 ? jj - 2 : 0][st], acc);
     } else {
       const bf16* arow = s.u.kr + (16 * rt + li) * kPitchR + 8 * lg;
 #pragma unroll
@@ -219,7 +251,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     }
     acc_job[jj] = acc;
   }
-  __syncthreads();  // k_raw row-major no longer needed; cumsum visible
+  lds_barrier();  // k_raw row-major no longer needed; cumsum visible
   if (tid < kC) {
     const int r = tid;
     const float eg = expf(s.gs[r]);
@@ -237,10 +269,8 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
   for (int jj = 0; jj < 5; ++jj) {
     const int job = wave + 4 * jj;
     const bool is_q = job >= 10;
-    int t = is_q ? job - 10 : job;
-    int rt = 0;
-    while (t > rt) { t -= rt + 1; ++rt; }
-    const int ct = t;
+    const int t = is_q ? job - 10 : job;
+    const int rt = tri_row(t), ct = tri_col(t);
     if (is_q) {
       // lane holds Aqk[i][j] for i = 16rt + li, j = 16ct + 4lg + r: exactly
       // half of its A-operand fragment (column block ct/2, half ct%2)
@@ -249,7 +279,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int j = 16 * ct + 4 * lg + r;
-        const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
+        const float decay = j <= i ? __builtin_amdgcn_exp2f((s.gs[i] - s.gs[j]) * kLog2e) : 0.f;
         const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
         bf16 hh, ll;
         split2(a, hh, ll);
@@ -264,29 +294,25 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = 16 * rt + 4 * lg + r;
-        const float decay = j <= i ? expf(s.gs[i] - s.gs[j]) : 0.f;
+        const float decay = j <= i ? __builtin_amdgcn_exp2f((s.gs[i] - s.gs[j]) * kLog2e) : 0.f;
         s.u.lm[i * kPitchF + j] =
             j < i ? (((s.kinv[i] * s.kinv[j]) * acc_job[jj][r]) * s.bs[i]) * decay : 0.f;
       }
     }
   }
-  for (int idx = tid; idx < 6 * 64; idx += 256) {   // the 6 upper tiles of Aqk
-    const int t = idx >> 6, ln = idx & 63;
-    const int rt = t < 3 ? 0 : (t < 5 ? 1 : 2);
-    const int ct = t < 3 ? t + 1 : (t < 5 ? t - 1 : 3);
-    const int o = frag_off(16 * rt + (ln & 15), 16 * ct + 4 * (ln >> 4), 2);
+  // Aqk's upper tiles (0, 1) and (2, 3) complete the A operands the scan
+  // uses (token tiles 0 and 2 with 32-token blocks 0 and 1); the other upper
+  // tiles are never used.
+  if (tid < 128) {
+    const int t = tid >> 6, ln = tid & 63;
+    const int o = frag_off(32 * t + (ln & 15), 32 * t + 16 + 4 * (ln >> 4), 2);
     *reinterpret_cast<bf16x4*>(ah + o) = bf16x4{};
     *reinterpret_cast<bf16x4*>(al + o) = bf16x4{};
   }
-  // zero the strictly-upper 16x16 tiles of L and T
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    const int i = idx >> 6, j = idx & 63;
-    if ((j >> 4) > (i >> 4)) {
-      s.u.lm[i * kPitchF + j] = 0.f;
-      s.tm[i * kPitchF + j] = 0.f;
-    }
-  }
-  __syncthreads();
+  // (The strictly-upper tiles of L are never read, and every entry of T is
+  // written below: S3 fills the diagonal blocks, S4 the lower blocks and
+  // clears the upper blocks it parks its sums in.)
+  lds_barrier();
 
   // S3. diagonal 16x16 blocks of T = (I + L)^-1: wave b inverts block b,
   // lane j < 16 owns column j (forward substitution, as fle:5207-5211).
@@ -303,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 #pragma unroll
     for (int i = 0; i < 16; ++i) s.tm[(16 * b + i) * kPitchF + 16 * b + j] = t[i];
   }
-  __syncthreads();
+  lds_barrier();
   // S4. off-diagonal blocks by distance d: T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj.
   // The intermediate sum is parked in the (still zero) upper block (j, i).
   for (int d = 1; d < 4; ++d) {
@@ -323,7 +349,7 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
         s.tm[(16 * bj + 4 * lg + r) * kPitchF + 16 * bi + li] = 0.f;
       }
     }
-    __syncthreads();
+    lds_barrier();
   }
 
   // S5. T diag(beta) as hi/lo A-operand fragments: 4 consecutive columns
