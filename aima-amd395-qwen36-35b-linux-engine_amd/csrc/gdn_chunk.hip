@@ -596,33 +596,34 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
   c_fetch_a(c_begin);
   lds_barrier();
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  // (a) publish the state tiles as the hi / lo B operands of tile pair w
+  // (for chunk c+1 this happens in (d) of chunk c, right after the update)
+  auto publish_state = [&]() {
+    bf16x8 hi, lo;
+    join_pair(split4(sreg[0]), split4(sreg[1]), hi, lo);
+    s.st[w][0][lane] = hi;
+    s.st[w][1][lane] = lo;
+  };
+  publish_state();
   for (unsigned c = c_begin; c < c_end; ++c) {
     const int par = c & 1;
     const unsigned nxt = c + 1 < last ? c + 1 : last;
-    // (a) publish the state tiles as the hi / lo B operands of tile pair w
-    {
-      bf16x8 hi, lo;
-      join_pair(split4(sreg[0]), split4(sreg[1]), hi, lo);
-      s.st[w][0][lane] = hi;
-      s.st[w][1][lane] = lo;
-    }
     lds_barrier();
-    // (b) Y = k_raw S, q_raw S (four independent accumulator chains: the hi
-    // and lo halves of S), Z = v - cy Y
+    // (b) Y = k_raw S (two accumulator chains: the hi and lo halves of S),
+    // Z = v - cy Y published first; q_raw S (needed only for the output)
+    // after it
     const float* sc = s.sc[par];
-    f32x4 ay = zero, aqs = zero, ay2 = zero, aqs2 = zero;
+    bf16x8 shi[4], slo[4];
+    f32x4 ay = zero, ay2 = zero;
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
-      const bf16x8 shi = s.st[k4][0][lane], slo = s.st[k4][1][lane];
+      shi[k4] = s.st[k4][0][lane];
+      slo[k4] = s.st[k4][1][lane];
       const bf16x8 kfa = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-      const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-      ay = mfma16x16x32(kfa, shi, ay);
-      aqs = mfma16x16x32(qfa, shi, aqs);
-      ay2 = mfma16x16x32(kfa, slo, ay2);
-      aqs2 = mfma16x16x32(qfa, slo, aqs2);
+      ay = mfma16x16x32(kfa, shi[k4], ay);
+      ay2 = mfma16x16x32(kfa, slo[k4], ay2);
     }
     ay += ay2;
-    aqs += aqs2;
     const int r0 = 16 * w + 4 * lg;
     const f32x4 cy = *reinterpret_cast<const f32x4*>(sc + kScCy * 64 + r0);
     const f32x4 rsq = *reinterpret_cast<const f32x4*>(sc + kScRsq * 64 + r0);
@@ -633,8 +634,15 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     for (int r = 0; r < 4; ++r)
       zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
     put_tile(s.z, w, lane, zv);
-    f32x4 acc = rsq * aqs;
     c_fetch_v(nxt);
+    f32x4 aqs = zero, aqs2 = zero;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+      const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+      aqs = mfma16x16x32(qfa, shi[k4], aqs);
+      aqs2 = mfma16x16x32(qfa, slo[k4], aqs2);
+    }
+    f32x4 acc = rsq * (aqs + aqs2);
     lds_barrier();
     // (c) v' = (T diag beta) Z: T is lower triangular, so token tiles 0, 1
     // only reduce over the first 32 tokens
@@ -654,18 +662,8 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
     c_fetch_t(nxt);
     lds_barrier();
-    // (d) o = rsq (q_raw S) + Aqk v'
-    f32x4 acc2 = zero, acc3 = zero;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      if (t2 == 1 && w < 2) break;
-      const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
-      acc = mfma16x16x32(ah[t2], vh, acc);
-      acc2 = mfma16x16x32(ah[t2], vl, acc2);
-      acc3 = mfma16x16x32(al[t2], vh, acc3);
-    }
-    acc += acc2 + acc3;
-    // S = exp(G_last) S + k_raw^T (rsk v')
+    // (d) S = exp(G_last) S + k_raw^T (rsk v'), published for chunk c+1
+    // at once; then this chunk's output o = rsq (q_raw S) + Aqk v'
     f32x4 sn[2] = {sreg[0] * egl, sreg[1] * egl};
     f32x4 sl[2] = {zero, zero};
 #pragma unroll
@@ -684,6 +682,17 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
     sreg[0] = sn[0] + sl[0];
     sreg[1] = sn[1] + sl[1];
+    if (c + 1 < c_end) publish_state();
+    f32x4 acc2 = zero, acc3 = zero;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      if (t2 == 1 && w < 2) break;
+      const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
+      acc = mfma16x16x32(ah[t2], vh, acc);
+      acc2 = mfma16x16x32(ah[t2], vl, acc2);
+      acc3 = mfma16x16x32(al[t2], vh, acc3);
+    }
+    acc += acc2 + acc3;
     c_fetch_a(nxt);
     // Output rows past the end fall outside the buffer range and are
     // dropped by the hardware (no branch, so no uncertain store count).
