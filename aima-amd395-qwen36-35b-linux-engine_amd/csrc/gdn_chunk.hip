@@ -605,6 +605,24 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     s.st[w][1][lane] = lo;
   };
   publish_state();
+  // A chunk's k fragments and row scalars, read from LDS at the end of the
+  // previous chunk (staged before its second barrier), so (b) starts with
+  // the state operands only.
+  bf16x8 kfa[4];
+  f32x4 cy, rsq, rsk;
+  float egl;
+  auto read_chunk = [&](unsigned c) {
+    const int par = c & 1;
+    const int r0 = 16 * w + 4 * lg;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+      kfa[k4] = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+    cy = *reinterpret_cast<const f32x4*>(s.sc[par] + kScCy * 64 + r0);
+    rsq = *reinterpret_cast<const f32x4*>(s.sc[par] + kScRsq * 64 + r0);
+    rsk = *reinterpret_cast<const f32x4*>(s.sc[par] + kScRsk * 64 + r0);
+    egl = s.sc[par][kScEgl * 64];
+  };
+  read_chunk(c_begin);
   for (unsigned c = c_begin; c < c_end; ++c) {
     const int par = c & 1;
     const unsigned nxt = c + 1 < last ? c + 1 : last;
@@ -612,23 +630,16 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     // (b) Y = k_raw S (two accumulator chains: the hi and lo halves of S),
     // Z = v - cy Y published first; q_raw S (needed only for the output)
     // after it
-    const float* sc = s.sc[par];
     bf16x8 shi[4], slo[4];
     f32x4 ay = zero, ay2 = zero;
 #pragma unroll
     for (int k4 = 0; k4 < 4; ++k4) {
       shi[k4] = s.st[k4][0][lane];
       slo[k4] = s.st[k4][1][lane];
-      const bf16x8 kfa = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-      ay = mfma16x16x32(kfa, shi[k4], ay);
-      ay2 = mfma16x16x32(kfa, slo[k4], ay2);
+      ay = mfma16x16x32(kfa[k4], shi[k4], ay);
+      ay2 = mfma16x16x32(kfa[k4], slo[k4], ay2);
     }
     ay += ay2;
-    const int r0 = 16 * w + 4 * lg;
-    const f32x4 cy = *reinterpret_cast<const f32x4*>(sc + kScCy * 64 + r0);
-    const f32x4 rsq = *reinterpret_cast<const f32x4*>(sc + kScRsq * 64 + r0);
-    const f32x4 rsk = *reinterpret_cast<const f32x4*>(sc + kScRsk * 64 + r0);
-    const float egl = sc[kScEgl * 64];
     f32x4 zv;
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -694,6 +705,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
     acc += acc2 + acc3;
     c_fetch_a(nxt);
+    if (c + 1 < c_end) read_chunk(c + 1);
     // Output rows past the end fall outside the buffer range and are
     // dropped by the hardware (no branch, so no uncertain store count).
     const unsigned tb = c * kC + 16 * w + 4 * lg;
