@@ -40,6 +40,26 @@ def test_chunk_prefill_matches_oracle(gpu, t, a_max, with_state):
     assert rel_err(st.cpu(), ref_s) <= TOL_STATE
 
 
+def test_chunk_prefill_repeated_heads_match_unrepeated(gpu):
+    """q/k given as 32 repeated heads (value head j reads head j) give the
+    same bits as the 16 key heads (value head j reads head j // 2): each
+    value head sees identical inputs, through the other head mapping."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(117)
+    t = 130
+    q, k, v, gg, beta = syn.gdn_core_inputs(t, g, a_max=4.0)
+    s0 = torch.randn(32, 128, 128, generator=g)
+    print(f"gdn chunk repeated heads T={t}", flush=True)
+    qd, kd, vd, gd, bd, sd = _to(gpu, q, k, v, gg, beta, s0)
+    o16, st16 = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+    q32 = qd.repeat_interleave(2, dim=-2).contiguous()
+    k32 = kd.repeat_interleave(2, dim=-2).contiguous()
+    o32, st32 = G.chunk_gated_delta_rule(q32, k32, vd, gd, bd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(o16, o32)
+    assert torch.equal(st16, st32)
+
+
 @pytest.mark.parametrize("t,a_max", [(1, 16.0), (5, 0.1), (64, 1.0)])
 def test_recurrent_matches_oracle(gpu, t, a_max):
     from qwen36_attn import gated_deltanet as G
