@@ -645,6 +645,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     for (int r = 0; r < 4; ++r)
       zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
     put_tile(s.z, w, lane, zv);
+    __builtin_amdgcn_sched_barrier(0);   // the exchange first, then the off-chain work
     c_fetch_v(nxt);
     f32x4 aqs = zero, aqs2 = zero;
 #pragma unroll
@@ -668,8 +669,8 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
         vp3 = mfma16x16x32(tl[t2], zh, vp3);
       }
       vp += vp2 + vp3;
-      put_tile(s.vp[0], w, lane, vp);
       put_tile(s.vp[1], w, lane, rsk * vp);
+      put_tile(s.vp[0], w, lane, vp);
     }
     c_fetch_t(nxt);
     lds_barrier();
@@ -694,6 +695,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     sreg[0] = sn[0] + sl[0];
     sreg[1] = sn[1] + sl[1];
     if (c + 1 < c_end) publish_state();
+    __builtin_amdgcn_sched_barrier(0);
     f32x4 acc2 = zero, acc3 = zero;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
