@@ -176,19 +176,27 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     for (int st = 0; st < 4; ++st) qpre[jq][st] = ldq(qrs, 16 * rt + li, 8 * lg + 32 * st);
   }
 
+  // S1 inputs: this thread's k and q row pieces, g and beta.  All loads
+  // are in flight before any is used (the sched_barrier keeps the compiler
+  // from deferring the q fragments behind the first waits: a second round
+  // trip).
+  const int r1 = tid >> 2, p1 = tid & 3;
+  const unsigned tok1 = tok0 + r1;
+  const bool valid1 = tok1 < tokens;
+  const unsigned tcl1 = valid1 ? tok1 : tokens - 1;
+  const float gval = g[(size_t)tcl1 * kGdnHv + h], bval = beta[(size_t)tcl1 * kGdnHv + h];
+  bf16x8 k8[4], q8[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k8[i] = ldq(krs, r1, 32 * p1 + 8 * i);
+    q8[i] = ldq(qrs, r1, 32 * p1 + 8 * i);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // S1. k rows -> LDS; l2 norms of k and q; g, beta.
   {
-    const int r = tid >> 2, p = tid & 3;
-    const unsigned tok = tok0 + r;
-    const bool valid = tok < tokens;
-    const unsigned tcl = valid ? tok : tokens - 1;
-    const float gval = g[(size_t)tcl * kGdnHv + h], bval = beta[(size_t)tcl * kGdnHv + h];
-    bf16x8 k8[4], q8[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      k8[i] = ldq(krs, r, 32 * p + 8 * i);
-      q8[i] = ldq(qrs, r, 32 * p + 8 * i);
-    }
+    const int r = r1, p = p1;
+    const bool valid = valid1;
     float kss = 0.f, qss = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -207,9 +215,11 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     if (p == 0) {
       s.kinv[r] = rsqrt_rn(kss + 1e-6f);
       s.qinv[r] = rsqrt_rn(qss + 1e-6f);
-      s.gs[r] = valid ? gval : 0.f;
-      s.bs[r] = valid ? bval : 0.f;
     }
+    // written by all four lanes of the row (the same value), so the g and
+    // beta loads are not sunk into a branch behind the first waits
+    s.gs[r] = valid ? gval : 0.f;
+    s.bs[r] = valid ? bval : 0.f;
   }
   lds_barrier();
   if (tid == 0) {  // sequential fp32 cumsum, as torch.cumsum (in registers)
