@@ -455,26 +455,34 @@ __device__ __forceinline__ bf16x8 frag_row(const bf16* m, int pitch, int row, in
   return bf16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
-// grid = 256 workgroups of 8 waves (32 heads x 8 groups of 16 v-columns; the
-// 8 groups of a head -- and the two heads of a key head -- share an XCD, so
-// a chunk's q, k and prep record come from HBM once per XCD).
-//  * Chain waves 0-3 (one per SIMD): wave w owns token tile w of every chunk
-//    and state tiles 2w, 2w+1 (rows 32w .. 32w+31), in the MFMA accumulator
-//    layout:  sreg[i][r] = S[16(2w+i) + 4lg + r][col].  Per chunk:
+// grid = 256 workgroups of 12 waves (32 heads x 8 groups of 16 v-columns;
+// the 8 groups of a head -- and the two heads of a key head -- share an
+// XCD, so a chunk's q, k and prep record come from HBM once per XCD).
+//  * Chain waves 0-3 (one per SIMD) carry the state recurrence only: wave w
+//    owns token tile w of every chunk and state tiles 2w, 2w+1 (rows
+//    32w .. 32w+31), in the MFMA accumulator layout:
+//    sreg[i][r] = S[16(2w+i) + 4lg + r][col].  Per chunk:
 //      (a) publish the state tiles (hi/lo);
-//      (b) Y = k_raw S and q_raw S for the wave's 16 tokens, publish
-//          Z = v - cy Y;
+//      (b) Y = k_raw S for the wave's 16 tokens, publish Z = v - cy Y;
 //      (c) v' = (T diag beta) Z for the wave's tokens; publish v', rsk v';
-//      (d) o = rsq (q S) + Aqk v', S = e^(G_last) S + k^T (rsk v').
-//  * Producer waves 4-7 (sharing the SIMDs, so their work fills the chain's
-//    stalls): in (a) of chunk c they stage chunk c+1's q rows and scalars
-//    into LDS (the chain reads a chunk's q and scalars in (b) only), in (b)
-//    its k rows (read by the chain up to (d)), and then request chunk c+2's
-//    rows.
+//      (d) S = e^(G_last) S + k^T (rsk v'), published for the next chunk.
+//  * Producer waves 4-7: in (a) of chunk c they stage chunk c+1's q rows
+//    and scalars into LDS (read from (b) of chunk c+1 on), in (b) its k
+//    rows (read by the chain from (d) of chunk c on), and then request
+//    chunk c+2's rows.
+//  * Output waves 8-11: token tile w's o = rsq (q_raw S) + Aqk v', with
+//    q_raw S in (b) (beside the chain's k_raw S, from the same published
+//    state) and Aqk v' and the store in (d).
+// The roles share the SIMDs, so each one's work fills the others' stalls;
+// the split was measured against others on MI355X (T = 8192, scan alone):
+// the chain also forming the output 187 us, the output on the producer
+// waves 238 us, these three roles 170 us; moving part of q_raw S into (c)
+// or part of the output into the next chunk's (b) put work on the chain's
+// busiest windows (264-279 us).
 // Each phase ends at a workgroup barrier, and every staged buffer is
 // double-buffered by chunk parity, so a buffer is rewritten only after the
 // barrier that follows its last read.
-__global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
+__global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     const char* __restrict__ ws, const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
     unsigned v_token_stride, const float* state_in, float* state_out,
@@ -486,7 +494,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
   const int kh = h * (int)qk_heads / kGdnHv;
   const int cg = slot & 7;
   const int tid = threadIdx.x, w = (tid >> 6) & 3, lane = tid & 63;
-  const bool producer = tid >= 256;
+  const bool producer = tid >= 256 && tid < 512, outputs = tid >= 512;
   const int li = lane & 15, lg = lane >> 4;
   const int col = 16 * cg + li;
   const unsigned last = c_end - 1;
@@ -572,9 +580,56 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
   };
 
-  // The two roles run separate loops (straight-line code per role, so the
+  // The three roles run separate loops (straight-line code per role, so the
   // compiler's in-order wait counts follow each role's own loads) with the
   // same barrier sequence: one after the prologue, three per chunk.
+  if (outputs) {
+    // Output waves 8-11: token tile w's o = rsq (q_raw S) + Aqk v'; q_raw S
+    // in (b) beside the chain's k_raw S (same published state), Aqk v' in
+    // (d) once v' is published.
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    c_fetch_a(c_begin);
+    lds_barrier();
+    for (unsigned c = c_begin; c < c_end; ++c) {
+      const int par = c & 1;
+      const unsigned nxt = c + 1 < last ? c + 1 : last;
+      lds_barrier();
+      {
+        f32x4 a1 = zero, a2 = zero;
+#pragma unroll
+        for (int k4 = 0; k4 < 4; ++k4) {
+          const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
+          a1 = mfma16x16x32(qfa, s.st[k4][0][lane], a1);
+          a2 = mfma16x16x32(qfa, s.st[k4][1][lane], a2);
+        }
+        const f32x4 rsq = *reinterpret_cast<const f32x4*>(s.sc[par] + kScRsq * 64 + 16 * w + 4 * lg);
+        acc = rsq * (a1 + a2);
+      }
+      lds_barrier();
+      lds_barrier();
+      f32x4 acc2 = zero, acc3 = zero;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        if (t2 == 1 && w < 2) break;
+        const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
+        acc = mfma16x16x32(ah[t2], vh, acc);
+        acc2 = mfma16x16x32(ah[t2], vl, acc2);
+        acc3 = mfma16x16x32(al[t2], vh, acc3);
+      }
+      acc += acc2 + acc3;
+      c_fetch_a(nxt);
+      // Output rows past the end fall outside the buffer range and are
+      // dropped by the hardware (no branch, so no uncertain store count).
+      const unsigned tb = c * kC + 16 * w + 4 * lg;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
+            (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
+    }
+    return;
+  }
   if (producer) {
     p_fetch(c_begin);
     p_stage(c_begin);
@@ -582,8 +637,9 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     p_fetch(c_begin + 1 < last ? c_begin + 1 : last);
     lds_barrier();
     for (unsigned c = c_begin; c < c_end; ++c) {
-      // (a) chunk c+1's q rows and scalars (last read by the chain in (b)
-      // of chunk c-1)
+      // (a) chunk c+1's q rows and scalars (the buffers of chunk c-1, whose
+      // q rows the output waves last read in (b) of chunk c-1 and whose
+      // scalars the chain read in (d) of chunk c-2)
       if (c + 1 < c_end) p_stage(c + 1);
       lds_barrier();
       // (b) chunk c+1's k rows (last read by the chain in (d) of chunk
@@ -603,7 +659,6 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
       sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
   c_fetch_v(c_begin);
   c_fetch_t(c_begin);
-  c_fetch_a(c_begin);
   lds_barrier();
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
   // (a) publish the state tiles as the hi / lo B operands of tile pair w
@@ -619,7 +674,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
   // previous chunk (staged before its second barrier), so (b) starts with
   // the state operands only.
   bf16x8 kfa[4];
-  f32x4 cy, rsq, rsk;
+  f32x4 cy, rsk;
   float egl;
   auto read_chunk = [&](unsigned c) {
     const int par = c & 1;
@@ -628,7 +683,6 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     for (int k4 = 0; k4 < 4; ++k4)
       kfa[k4] = frag_row(s.kr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
     cy = *reinterpret_cast<const f32x4*>(s.sc[par] + kScCy * 64 + r0);
-    rsq = *reinterpret_cast<const f32x4*>(s.sc[par] + kScRsq * 64 + r0);
     rsk = *reinterpret_cast<const f32x4*>(s.sc[par] + kScRsk * 64 + r0);
     egl = s.sc[par][kScEgl * 64];
   };
@@ -638,8 +692,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     const unsigned nxt = c + 1 < last ? c + 1 : last;
     lds_barrier();
     // (b) Y = k_raw S (two accumulator chains: the hi and lo halves of S),
-    // Z = v - cy Y published first; q_raw S (needed only for the output)
-    // after it
+    // Z = v - cy Y published
     bf16x8 shi[4], slo[4];
     f32x4 ay = zero, ay2 = zero;
 #pragma unroll
@@ -655,16 +708,7 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     for (int r = 0; r < 4; ++r)
       zv[r] = bf2f(__builtin_bit_cast(bf16, (unsigned short)vv[r])) - cy[r] * ay[r];
     put_tile(s.z, w, lane, zv);
-    __builtin_amdgcn_sched_barrier(0);   // the exchange first, then the off-chain work
     c_fetch_v(nxt);
-    f32x4 aqs = zero, aqs2 = zero;
-#pragma unroll
-    for (int k4 = 0; k4 < 4; ++k4) {
-      const bf16x8 qfa = frag_row(s.qr[par], kPitchR, 16 * w + li, 32 * k4 + 4 * lg);
-      aqs = mfma16x16x32(qfa, shi[k4], aqs);
-      aqs2 = mfma16x16x32(qfa, slo[k4], aqs2);
-    }
-    f32x4 acc = rsq * (aqs + aqs2);
     lds_barrier();
     // (c) v' = (T diag beta) Z: T is lower triangular, so token tiles 0, 1
     // only reduce over the first 32 tokens
@@ -684,8 +728,8 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
     c_fetch_t(nxt);
     lds_barrier();
-    // (d) S = exp(G_last) S + k_raw^T (rsk v'), published for chunk c+1
-    // at once; then this chunk's output o = rsq (q_raw S) + Aqk v'
+    // (d) S = exp(G_last) S + k_raw^T (rsk v'), published for chunk c+1,
+    // and chunk c+1's k fragments and scalars
     f32x4 sn[2] = {sreg[0] * egl, sreg[1] * egl};
     f32x4 sl[2] = {zero, zero};
 #pragma unroll
@@ -704,28 +748,10 @@ __global__ __launch_bounds__(512, 1) void gdn_chunk_scan_kernel(
     }
     sreg[0] = sn[0] + sl[0];
     sreg[1] = sn[1] + sl[1];
-    if (c + 1 < c_end) publish_state();
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 acc2 = zero, acc3 = zero;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      if (t2 == 1 && w < 2) break;
-      const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
-      acc = mfma16x16x32(ah[t2], vh, acc);
-      acc2 = mfma16x16x32(ah[t2], vl, acc2);
-      acc3 = mfma16x16x32(al[t2], vh, acc3);
+    if (c + 1 < c_end) {
+      publish_state();
+      read_chunk(c + 1);
     }
-    acc += acc2 + acc3;
-    c_fetch_a(nxt);
-    if (c + 1 < c_end) read_chunk(c + 1);
-    // Output rows past the end fall outside the buffer range and are
-    // dropped by the hardware (no branch, so no uncertain store count).
-    const unsigned tb = c * kC + 16 * w + 4 * lg;
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_buffer_store_b16(
-          __builtin_bit_cast(unsigned short, f2bf(acc[r])), out_rsrc,
-          (int)((((tb + r) * kGdnHv + h) * kGdnDv + col) * 2), 0, 0);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i)
@@ -783,7 +809,7 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   // CU's LDS, so a concurrent prep would only delay them.
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256), sizeof(PrepLds), st,
                      qb, kb, qk_heads, qk_token_stride, gb, bb, tokens, wsb, 0u);
-  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(512),
+  hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(768),
                      sizeof(ScanLds), st, wsb, qb, kb, vb, qk_heads, qk_token_stride,
                      v_token_stride, static_cast<const float*>(state_in), so,
                      static_cast<bf16*>(out), tokens, 0u, n_chunks);
