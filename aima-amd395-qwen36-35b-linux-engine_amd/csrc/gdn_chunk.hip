@@ -364,8 +364,11 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
 
   // S5. T diag(beta) as hi/lo A-operand fragments: 4 consecutive columns
   // are 4 consecutive elements of a fragment.
+  // Rows 0-31 against columns 32-63 (the second 32-token block of token
+  // tiles 0 and 1) are zero and never read by the scan: not stored.
   for (int idx = tid; idx < kC * 16; idx += 256) {
     const int i = idx >> 4, j0 = 4 * (idx & 15);
+    if (i < 32 && j0 >= 32) continue;
     const f32x4 t4 = *reinterpret_cast<const f32x4*>(s.tm + i * kPitchF + j0);
     const f32x4 b4 = *reinterpret_cast<const f32x4*>(s.bs + j0);
     bf16x4 hv, lv;
@@ -559,6 +562,8 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
       vv[r] = __builtin_amdgcn_raw_buffer_load_b16(
           vrs, (int)(((16 * w + 4 * lg + r) * v_token_stride + li) * 2), 0, 0);
   };
+  // (Token tiles 0 and 1 also load the second 32-token block, which the
+  // prep does not store and they never use: the loads stay unconditional.)
   auto c_fetch_t = [&](unsigned c) {
     const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
     const bf16x8* Th = reinterpret_cast<const bf16x8*>(b + kOffTh) + 128 * w + lane;
