@@ -34,17 +34,20 @@
 //    that is sequential inside a chunk -- T = (I+L)^-1, formed blockwise
 //    (16x16 diagonal blocks by forward substitution, off-diagonal blocks by
 //    fp32 MFMA products) -- stored as T diag(beta) in hi/lo bf16 A-operand
-//    fragments, plus the chunk's per-token scalars (G, kinv, q scale, row
-//    scales, exp(G_last)): an 18 KB record per (chunk, head).
+//    fragments, Aqk in the same form, and the chunk's per-token scalars (G,
+//    kinv, q scale, row scales, exp(G_last)): a 34,560-byte record per
+//    (chunk, head).
 //  * gdn_chunk_scan (grid = 32 heads x 8 groups of 16 v-columns, sequential
-//    over chunks): reads q, k, v of each chunk straight from the inputs
-//    (staged through LDS) and the chunk's prep record; wave w owns token tile
-//    w of each chunk and state rows 32w .. 32w+31 of its 16 columns, in
-//    registers in the MFMA accumulator layout.  That layout is also the
-//    B-operand layout of the next products (the reduction index -- state row
-//    or token -- is permuted to match, and the A operands are read in the
-//    same order), so per chunk only the state tiles, (v - ..) and v' (hi/lo
-//    bf16) pass between waves through LDS.
+//    over chunks, 12 waves in three roles): producer waves stage each
+//    chunk's q and k rows (read straight from the inputs) and scalars into
+//    LDS a chunk ahead; chain wave w owns token tile w of each chunk and
+//    state rows 32w .. 32w+31 of its 16 columns, in registers in the MFMA
+//    accumulator layout, and carries the recurrence; output wave w forms
+//    token tile w's output from the published state and v'.  The
+//    accumulator layout is also the B-operand layout of the next products
+//    (the reduction index -- state row or token -- is permuted to match, and
+//    the A operands are read in the same order), so per chunk only the state
+//    tiles, (v - ..) and v' (hi/lo bf16) pass between waves through LDS.
 #include "common.h"
 
 #include <mutex>
