@@ -549,11 +549,9 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     if (pt < kNsc * 16) reinterpret_cast<u32x4*>(s.sc[par])[pt] = psc;
   };
   // ---- chain side -----------------------------------------------------------
-  const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      out, 0, (int)(tokens * kGdnHv * kGdnDv * 2), 0x00020000);
   const size_t sb = (size_t)h * kGdnDk * kGdnDv + col;
   f32x4 sreg[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-  bf16x8 th[2], tl[2], ah[2], al[2];
+  bf16x8 th[2], tl[2];
   unsigned vv[4];
   auto c_fetch_v = [&](unsigned c) {
     const unsigned rows = min((unsigned)kC, tokens - c * kC);
@@ -577,16 +575,6 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
       tl[t2] = Tl[64 * t2];
     }
   };
-  auto c_fetch_a = [&](unsigned c) {
-    const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
-    const bf16x8* Ah = reinterpret_cast<const bf16x8*>(b + kOffAh) + 128 * w + lane;
-    const bf16x8* Al = reinterpret_cast<const bf16x8*>(b + kOffAl) + 128 * w + lane;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      ah[t2] = Ah[64 * t2];
-      al[t2] = Al[64 * t2];
-    }
-  };
 
   // The three roles run separate loops (straight-line code per role, so the
   // compiler's in-order wait counts follow each role's own loads) with the
@@ -595,8 +583,21 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     // Output waves 8-11: token tile w's o = rsq (q_raw S) + Aqk v'; q_raw S
     // in (b) beside the chain's k_raw S (same published state), Aqk v' in
     // (d) once v' is published.
+    const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out, 0, (int)(tokens * kGdnHv * kGdnDv * 2), 0x00020000);
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    bf16x8 ah[2], al[2];   // token tile w's rows of Aqk (hi / lo), 32-token blocks
+    auto c_fetch_a = [&](unsigned c) {
+      const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
+      const bf16x8* Ah = reinterpret_cast<const bf16x8*>(b + kOffAh) + 128 * w + lane;
+      const bf16x8* Al = reinterpret_cast<const bf16x8*>(b + kOffAl) + 128 * w + lane;
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        ah[t2] = Ah[64 * t2];
+        al[t2] = Al[64 * t2];
+      }
+    };
     c_fetch_a(c_begin);
     lds_barrier();
     for (unsigned c = c_begin; c < c_end; ++c) {
