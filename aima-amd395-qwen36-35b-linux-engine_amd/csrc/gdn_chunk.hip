@@ -563,17 +563,18 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
       vv[r] = __builtin_amdgcn_raw_buffer_load_b16(
           vrs, (int)(((16 * w + 4 * lg + r) * v_token_stride + li) * 2), 0, 0);
   };
-  // (Token tiles 0 and 1 also load the second 32-token block, which the
-  // prep does not store and they never use: the loads stay unconditional.)
+  // (Token tiles 0 and 1 never use the second 32-token block, which the prep
+  // does not store: their second load re-reads the first block, so the loads
+  // stay unconditional and no unwritten workspace byte is read.)
+  const int t2_hi = w < 2 ? 0 : 64;
   auto c_fetch_t = [&](unsigned c) {
     const char* b = ws + ((size_t)c * kGdnHv + h) * kUnitBytes;
     const bf16x8* Th = reinterpret_cast<const bf16x8*>(b + kOffTh) + 128 * w + lane;
     const bf16x8* Tl = reinterpret_cast<const bf16x8*>(b + kOffTl) + 128 * w + lane;
-#pragma unroll
-    for (int t2 = 0; t2 < 2; ++t2) {
-      th[t2] = Th[64 * t2];
-      tl[t2] = Tl[64 * t2];
-    }
+    th[0] = Th[0];
+    tl[0] = Tl[0];
+    th[1] = Th[t2_hi];
+    tl[1] = Tl[t2_hi];
   };
 
   // The three roles run separate loops (straight-line code per role, so the

@@ -266,3 +266,23 @@ def test_config4_conv_from_mixed_qkv_then_chunk_prefill(gpu):
                                             torch.zeros(1, 32, 128, 128))
     assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
     assert rel_err(st.cpu(), ref_s) <= TOL_STATE
+
+
+def test_chunk_prefill_ignores_stale_workspace(gpu):
+    """The chunked prefill's result does not depend on what the workspace held
+    before the call: a workspace pre-filled with NaN bytes gives the same bits
+    as a fresh call (the prep writes every record byte the scan reads)."""
+    from qwen36_attn import gated_deltanet as G
+    from qwen36_attn import _tensors
+    t = 200
+    g = syn.gen(321)
+    q, k, v, gg, beta = syn.gdn_core_inputs(t, g, a_max=1.0)
+    s0 = torch.randn(32, 128, 128, generator=g)
+    qd, kd, vd, gd, bd, sd = _to(gpu, q, k, v, gg, beta, s0)
+    print("gdn chunk stale workspace T=200", flush=True)
+    out1, st1 = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+    out1, st1 = out1.clone(), st1.clone()
+    _tensors._SCRATCH[("gdn_chunk", gpu.index or 0)].fill_(0xFF)   # every float NaN
+    out2, st2 = G.chunk_gated_delta_rule(qd, kd, vd, gd, bd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(out1, out2) and torch.equal(st1, st2)
