@@ -131,3 +131,18 @@ def test_decode_step_equals_norm_rope_then_decode(gpu, cache_end, position, spli
     torch.cuda.synchronize()
     assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
     assert torch.equal(fused, ref)
+
+
+def test_decode_ignores_stale_workspace(gpu):
+    """A decode's result does not depend on what the shared split-partial
+    workspace held before the call: NaN-filled scratch gives the same bits."""
+    from qwen36_attn.full_attention import decode_gqa
+    from qwen36_attn import _tensors
+    q, k, v = _inputs(5000, seed=77)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    print("decode stale workspace cache_end=4999", flush=True)
+    a = decode_gqa(qd, kd, vd, 4998, 4999).clone()
+    _tensors._SCRATCH[("decode_gqa", gpu.index or 0)].fill_(0xFF)   # every float NaN
+    b = decode_gqa(qd, kd, vd, 4998, 4999)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -263,3 +263,19 @@ def test_config3_norm_rope_kv_write_and_gated_output(gpu):
         a = O.prefill_attention(qh[r:r + 1], kc[:lim], vc[:lim], lim - 1, out_dtype=torch.float32)
         ref = O.output_gate(a.to(torch.bfloat16), gate_ref[r:r + 1])
         assert (gated[r:r + 1].float() - ref.float()).abs().max().item() <= TOL, r
+
+
+def test_split_prefill_ignores_stale_workspace(gpu):
+    """A short prompt (split key ranges + combine through the shared scratch)
+    does not depend on what the scratch held before the call: NaN-filled
+    scratch gives the same bits."""
+    from qwen36_attn.full_attention import fmha_prefill
+    from qwen36_attn import _tensors
+    q, k, v = _inputs(700, 1500, seed=55)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    print("prefill stale workspace T=700 S=1500", flush=True)
+    a = fmha_prefill(qd, kd, vd).clone()
+    _tensors._SCRATCH[("fmha_split", gpu.index or 0)].fill_(0xFF)   # every float NaN
+    b = fmha_prefill(qd, kd, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
