@@ -129,3 +129,27 @@ def test_moe_prefill_max_tokens_sampled_rows(gpu):
     assert (out[rows].cpu().float() - ref.float()).abs().max().item() <= TOL
     del inp, attn, out, block
     torch.cuda.empty_cache()
+
+
+def test_moe_prefill_and_decode_ignore_stale_workspace(gpu):
+    """The MoE block's results do not depend on what its shared workspaces
+    (routing ids, histograms, aligned row lists, activations, partial rows)
+    held before the call: 0xFF-filled scratch gives the same bits."""
+    from qwen36_attn.moe import MoEBlock
+    from qwen36_attn import _tensors
+    g = syn.gen(620)
+    w = syn.moe_weights(g, n_experts=32)
+    inp = syn.randn((37, 2048), g, 0.5).to(gpu)
+    attn = syn.randn((37, 2048), g, 0.5).to(gpu)
+    block = MoEBlock({k: v.to(gpu) for k, v in w.items()})
+    print("moe stale workspace T=37 E=32", flush=True)
+    a = block.prefill(inp, attn).clone()
+    d = block.decode(inp[:1], attn[:1]).clone()
+    torch.cuda.synchronize()
+    dev = gpu.index or 0
+    _tensors._SCRATCH[("moe_prefill", dev)].fill_(0xFF)
+    _tensors._SCRATCH[("moe_decode", dev)].fill_(0xFF)
+    b = block.prefill(inp, attn)
+    e = block.decode(inp[:1], attn[:1])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(d, e)
