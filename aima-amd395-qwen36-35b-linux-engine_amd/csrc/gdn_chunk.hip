@@ -365,26 +365,33 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     lds_barrier();
   }
 
-  // S5. T diag(beta) as hi/lo A-operand fragments: 4 consecutive columns
-  // are 4 consecutive elements of a fragment.
-  // Rows 0-31 against columns 32-63 (the second 32-token block of token
-  // tiles 0 and 1) are zero and never read by the scan: not stored.
-  for (int idx = tid; idx < kC * 16; idx += 256) {
-    const int i = idx >> 4, j0 = 4 * (idx & 15);
-    if (i < 32 && j0 >= 32) continue;
-    const f32x4 t4 = *reinterpret_cast<const f32x4*>(s.tm + i * kPitchF + j0);
-    const f32x4 b4 = *reinterpret_cast<const f32x4*>(s.bs + j0);
-    bf16x4 hv, lv;
+  // S5. T diag(beta) as hi/lo A-operand fragments: item (row i, 32-token
+  // block kb, group g) forms columns 32kb + 4g .. +3 and 32kb + 16 + 4g .. +3,
+  // the 8 elements of one fragment slot, stored as one 16-byte write per
+  // plane.  Rows 0-31 against columns 32-63 (the second 32-token block of
+  // token tiles 0 and 1) are zero and never read by the scan: not stored.
+  for (int idx = tid; idx < kC * 8; idx += 256) {
+    const int i = idx >> 3, kb = (idx >> 2) & 1, g = idx & 3;
+    if (i < 32 && kb == 1) continue;
+    const int j0 = 32 * kb + 4 * g;
+    const f32x4 ta = *reinterpret_cast<const f32x4*>(s.tm + i * kPitchF + j0);
+    const f32x4 tb = *reinterpret_cast<const f32x4*>(s.tm + i * kPitchF + j0 + 16);
+    const f32x4 ba = *reinterpret_cast<const f32x4*>(s.bs + j0);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(s.bs + j0 + 16);
+    bf16x8 hv, lv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       bf16 hh, ll;
-      split2(t4[e] * b4[e], hh, ll);
+      split2(ta[e] * ba[e], hh, ll);
       hv[e] = hh;
       lv[e] = ll;
+      split2(tb[e] * bb[e], hh, ll);
+      hv[4 + e] = hh;
+      lv[4 + e] = ll;
     }
     const int o = frag_off(i, j0, 2);
-    *reinterpret_cast<bf16x4*>(th + o) = hv;
-    *reinterpret_cast<bf16x4*>(tl + o) = lv;
+    *reinterpret_cast<bf16x8*>(th + o) = hv;
+    *reinterpret_cast<bf16x8*>(tl + o) = lv;
   }
 }
 
