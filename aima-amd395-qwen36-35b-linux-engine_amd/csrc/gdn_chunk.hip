@@ -56,6 +56,13 @@ namespace q36 {
 namespace {
 
 constexpr int kC = 64;
+// qwen36_gdn_chunk_prefill_ex flags (same values as the public header's)
+constexpr unsigned kFlagQkNormalized = 1u;   // q, k already l2-normalised
+constexpr unsigned kFlagStateVk = 2u;        // states in [Hv, dv, dk] order
+
+__host__ __forceinline__ bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
 constexpr int kPitchR = 136;   // bf16 row pitch (272 B) of [64][128] tiles
 constexpr int kPitchF = 68;    // fp32 row pitch of [64][64] matrices
 constexpr float kQScale = 0.08838834764831845f;   // 1/sqrt(128)
@@ -140,7 +147,8 @@ __device__ __forceinline__ int tri_col(int t) {
 __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, unsigned qk_heads,
     unsigned qk_token_stride, const float* __restrict__ g,
-    const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws, unsigned c0) {
+    const float* __restrict__ beta, unsigned tokens, char* __restrict__ ws, unsigned c0,
+    bool l2norm) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   PrepLds& s = *reinterpret_cast<PrepLds*>(smem);
   const unsigned c = c0 + blockIdx.x;
@@ -215,9 +223,9 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     kss += __shfl_xor(kss, 2, 64);
     qss += __shfl_xor(qss, 1, 64);
     qss += __shfl_xor(qss, 2, 64);
-    if (p == 0) {
-      s.kinv[r] = rsqrt_rn(kss + 1e-6f);
-      s.qinv[r] = rsqrt_rn(qss + 1e-6f);
+    if (p == 0) {   // q, k already unit-norm (vLLM's use_qk_l2norm_in_kernel=False): 1
+      s.kinv[r] = l2norm ? rsqrt_rn(kss + 1e-6f) : 1.f;
+      s.qinv[r] = l2norm ? rsqrt_rn(qss + 1e-6f) : 1.f;
     }
     // written by all four lanes of the row (the same value), so the g and
     // beta loads are not sunk into a branch behind the first waits
@@ -499,7 +507,8 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     const char* __restrict__ ws, const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, unsigned qk_heads, unsigned qk_token_stride,
     unsigned v_token_stride, const float* state_in, float* state_out,
-    bf16* __restrict__ out, unsigned tokens, unsigned c_begin, unsigned c_end) {
+    bf16* __restrict__ out, unsigned tokens, unsigned c_begin, unsigned c_end,
+    bool state_vk) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   ScanLds& s = *reinterpret_cast<ScanLds*>(smem);
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
@@ -556,7 +565,9 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     if (pt < kNsc * 16) reinterpret_cast<u32x4*>(s.sc[par])[pt] = psc;
   };
   // ---- chain side -----------------------------------------------------------
-  const size_t sb = (size_t)h * kGdnDk * kGdnDv + col;
+  // state element (k row, v column): [Hv, dk, dv], or vLLM's [Hv, dv, dk]
+  const size_t srow = state_vk ? 1 : kGdnDv;
+  const size_t sb = (size_t)h * kGdnDk * kGdnDv + (size_t)col * (state_vk ? kGdnDk : 1);
   f32x4 sreg[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
   bf16x8 th[2], tl[2];
   unsigned vv[4];
@@ -673,7 +684,7 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] : 0.f;
+      sreg[i][r] = state_in ? state_in[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * srow] : 0.f;
   c_fetch_v(c_begin);
   c_fetch_t(c_begin);
   lds_barrier();
@@ -774,7 +785,7 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * kGdnDv] = sreg[i][r];
+      state_out[sb + (size_t)(16 * (2 * w + i) + 4 * lg + r) * srow] = sreg[i][r];
 }
 
 }  // namespace
@@ -787,18 +798,20 @@ Q36_EXPORT size_t qwen36_gdn_chunk_prefill_workspace_bytes(unsigned tokens) {
   return n_chunks * kGdnHv * kUnitBytes;
 }
 
-Q36_EXPORT int qwen36_gdn_chunk_prefill(
+Q36_EXPORT int qwen36_gdn_chunk_prefill_ex(
     const void* q, const void* k, const void* v, unsigned qk_heads,
     unsigned qk_token_stride, unsigned v_token_stride, const void* g,
     const void* beta, const void* state_in, void* state_out, void* out,
-    unsigned tokens, void* workspace, size_t workspace_bytes, void* stream) {
+    unsigned tokens, unsigned flags, void* workspace, size_t workspace_bytes, void* stream) {
   if (q == nullptr || k == nullptr || v == nullptr || g == nullptr ||
       beta == nullptr || state_out == nullptr || out == nullptr ||
       workspace == nullptr || tokens == 0 || tokens > kMaxTokens ||
+      (flags & ~(kFlagQkNormalized | kFlagStateVk)) != 0 ||
       (qk_heads != 16u && qk_heads != 32u) ||
       qk_token_stride < qk_heads * kGdnDk ||
       v_token_stride < (unsigned)(kGdnHv * kGdnDv) ||
-      (qk_token_stride % 8) != 0 || (v_token_stride % 8) != 0)
+      (qk_token_stride % 8) != 0 || (v_token_stride % 8) != 0 ||
+      !aligned16(q) || !aligned16(k) || !aligned16(v))
     return Q36_EINVAL;
   const unsigned n_chunks = (tokens + kC - 1) / kC;
   if (workspace_bytes < (size_t)n_chunks * kGdnHv * kUnitBytes) return Q36_EINVAL;
@@ -822,13 +835,25 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill(
   const float* gb = static_cast<const float*>(g);
   const float* bb = static_cast<const float*>(beta);
   float* so = static_cast<float*>(state_out);
+  const bool l2norm = (flags & kFlagQkNormalized) == 0;
+  const bool state_vk = (flags & kFlagStateVk) != 0;
   // Prep over every chunk, then the scan: the scan's workgroups take a whole
   // CU's LDS, so a concurrent prep would only delay them.
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256), sizeof(PrepLds), st,
-                     qb, kb, qk_heads, qk_token_stride, gb, bb, tokens, wsb, 0u);
+                     qb, kb, qk_heads, qk_token_stride, gb, bb, tokens, wsb, 0u, l2norm);
   hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(768),
                      sizeof(ScanLds), st, wsb, qb, kb, vb, qk_heads, qk_token_stride,
                      v_token_stride, static_cast<const float*>(state_in), so,
-                     static_cast<bf16*>(out), tokens, 0u, n_chunks);
+                     static_cast<bf16*>(out), tokens, 0u, n_chunks, state_vk);
   return static_cast<int>(hipGetLastError());
+}
+
+Q36_EXPORT int qwen36_gdn_chunk_prefill(
+    const void* q, const void* k, const void* v, unsigned qk_heads,
+    unsigned qk_token_stride, unsigned v_token_stride, const void* g,
+    const void* beta, const void* state_in, void* state_out, void* out,
+    unsigned tokens, void* workspace, size_t workspace_bytes, void* stream) {
+  return qwen36_gdn_chunk_prefill_ex(q, k, v, qk_heads, qk_token_stride, v_token_stride, g, beta,
+                                     state_in, state_out, out, tokens, 0u, workspace,
+                                     workspace_bytes, stream);
 }

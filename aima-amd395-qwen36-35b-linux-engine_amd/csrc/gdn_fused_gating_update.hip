@@ -35,8 +35,26 @@ __global__ __launch_bounds__(kFguRows * kFguLanesPerRow) void gdn_fused_gating_u
     const bf16* __restrict__ k, unsigned qk_heads, unsigned qk_token_stride,
     const bf16* __restrict__ v, unsigned v_token_stride, const float* state_in,
     float* state_out, bf16* __restrict__ out, unsigned tokens, float scale,
-    bool l2norm) {
+    bool l2norm, const int* __restrict__ cu_seqlens, const int* __restrict__ state_indices,
+    unsigned n_slots) {
   const int h = blockIdx.x;
+  const unsigned seq = blockIdx.z;
+  unsigned t_begin = 0, t_end = tokens;
+  size_t slot = 0;
+  if (gridDim.z > 1 || cu_seqlens != nullptr || state_indices != nullptr) {
+    if (cu_seqlens != nullptr) {
+      t_begin = (unsigned)max(cu_seqlens[seq], 0);
+      t_end = min((unsigned)max(cu_seqlens[seq + 1], 0), tokens);
+    } else {
+      t_begin = seq;
+      t_end = seq + 1;
+    }
+    const int sl = state_indices != nullptr ? state_indices[seq] : (int)seq;
+    if (sl < 0 || (unsigned)sl >= n_slots || t_begin >= t_end) return;   // padding
+    slot = (size_t)sl * kGdnHv * kGdnDv * kGdnDk;
+  }
+  state_in += slot;
+  state_out += slot;
   const int row = blockIdx.y * kFguRows + (threadIdx.x / kFguLanesPerRow);
   const int part = threadIdx.x % kFguLanesPerRow;
   const int c0 = part * kFguCols;
@@ -51,7 +69,7 @@ __global__ __launch_bounds__(kFguRows * kFguLanesPerRow) void gdn_fused_gating_u
   }
   const float A = expf(a_log[h]);
   const float dtb = dt_bias[h];
-  for (unsigned t = 0; t < tokens; ++t) {
+  for (unsigned t = t_begin; t < t_end; ++t) {
     // every per-token input is requested up front (one memory round trip)
     const bf16x8* qp = reinterpret_cast<const bf16x8*>(q + (size_t)t * qk_token_stride + kh * kGdnDk + c0);
     const bf16x8* kp = reinterpret_cast<const bf16x8*>(k + (size_t)t * qk_token_stride + kh * kGdnDk + c0);
@@ -105,15 +123,17 @@ __global__ __launch_bounds__(kFguRows * kFguLanesPerRow) void gdn_fused_gating_u
 
 using namespace q36;
 
-Q36_EXPORT int qwen36_gdn_fused_gating_update(
-    const void* a_log, const void* a, const void* b, unsigned ab_row_stride,
-    const void* dt_bias, const void* q, const void* k, unsigned qk_heads,
-    unsigned qk_token_stride, const void* v, unsigned v_token_stride,
-    const void* state_in, void* state_out, void* out, unsigned tokens,
-    float scale, unsigned flags, void* stream) {
+namespace {
+int fgu_launch(const void* a_log, const void* a, const void* b, unsigned ab_row_stride,
+               const void* dt_bias, const void* q, const void* k, unsigned qk_heads,
+               unsigned qk_token_stride, const void* v, unsigned v_token_stride,
+               const void* state_in, void* state_out, void* out, unsigned tokens,
+               const int* cu_seqlens, const int* state_indices, unsigned n_seqs,
+               unsigned n_slots, float scale, unsigned flags, void* stream) {
   if (a_log == nullptr || a == nullptr || b == nullptr || dt_bias == nullptr ||
       q == nullptr || k == nullptr || v == nullptr || state_in == nullptr ||
       state_out == nullptr || out == nullptr || tokens == 0 || tokens > kMaxTokens ||
+      n_seqs == 0 || n_seqs > 65535u || n_slots == 0 ||
       (qk_heads != 16u && qk_heads != 32u) || ab_row_stride < (unsigned)kGdnHv ||
       qk_token_stride < qk_heads * kGdnDk || (qk_token_stride % 8) != 0 ||
       v_token_stride < (unsigned)(kGdnHv * kGdnDv) || (flags & ~1u) != 0 ||
@@ -123,13 +143,40 @@ Q36_EXPORT int qwen36_gdn_fused_gating_update(
       (reinterpret_cast<uintptr_t>(state_out) % 16) != 0)
     return Q36_EINVAL;
   hipLaunchKernelGGL(gdn_fused_gating_update_kernel,
-                     dim3(kGdnHv, kGdnDv / kFguRows), dim3(kFguRows * kFguLanesPerRow), 0,
+                     dim3(kGdnHv, kGdnDv / kFguRows, n_seqs), dim3(kFguRows * kFguLanesPerRow), 0,
                      static_cast<hipStream_t>(stream), static_cast<const float*>(a_log),
                      static_cast<const bf16*>(a), static_cast<const bf16*>(b), ab_row_stride,
                      static_cast<const float*>(dt_bias), static_cast<const bf16*>(q),
                      static_cast<const bf16*>(k), qk_heads, qk_token_stride,
                      static_cast<const bf16*>(v), v_token_stride,
                      static_cast<const float*>(state_in), static_cast<float*>(state_out),
-                     static_cast<bf16*>(out), tokens, scale, (flags & 1u) != 0);
+                     static_cast<bf16*>(out), tokens, scale, (flags & 1u) != 0, cu_seqlens,
+                     state_indices, n_slots);
   return static_cast<int>(hipGetLastError());
+}
+}  // namespace
+
+Q36_EXPORT int qwen36_gdn_fused_gating_update(
+    const void* a_log, const void* a, const void* b, unsigned ab_row_stride,
+    const void* dt_bias, const void* q, const void* k, unsigned qk_heads,
+    unsigned qk_token_stride, const void* v, unsigned v_token_stride,
+    const void* state_in, void* state_out, void* out, unsigned tokens,
+    float scale, unsigned flags, void* stream) {
+  return fgu_launch(a_log, a, b, ab_row_stride, dt_bias, q, k, qk_heads, qk_token_stride, v,
+                    v_token_stride, state_in, state_out, out, tokens, nullptr, nullptr, 1u, 1u,
+                    scale, flags, stream);
+}
+
+Q36_EXPORT int qwen36_gdn_fused_gating_update_varlen(
+    const void* a_log, const void* a, const void* b, unsigned ab_row_stride,
+    const void* dt_bias, const void* q, const void* k, unsigned qk_heads,
+    unsigned qk_token_stride, const void* v, unsigned v_token_stride,
+    const void* state_in, void* state_out, void* out, unsigned tokens,
+    const void* cu_seqlens, const void* state_indices, unsigned n_seqs, unsigned n_slots,
+    float scale, unsigned flags, void* stream) {
+  if (cu_seqlens == nullptr && n_seqs != tokens) return Q36_EINVAL;
+  return fgu_launch(a_log, a, b, ab_row_stride, dt_bias, q, k, qk_heads, qk_token_stride, v,
+                    v_token_stride, state_in, state_out, out, tokens,
+                    static_cast<const int*>(cu_seqlens), static_cast<const int*>(state_indices),
+                    n_seqs, n_slots, scale, flags, stream);
 }

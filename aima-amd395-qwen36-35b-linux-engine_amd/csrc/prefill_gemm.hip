@@ -284,7 +284,9 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void*
 }
 
 Q36_EXPORT size_t qwen36_prefill_gemm_workspace_bytes(unsigned m, unsigned n, unsigned k) {
-  if (m == 0 || n == 0 || k == 0 || (k % 64) != 0) return 0;
+  if (m == 0 || n == 0 || k == 0 || m > kMaxTokens || n > 65536u || k > 16384u ||
+      (k % 64) != 0)
+    return 0;   // geometry the launch rejects
   return splitk_bytes(m, n, gemm_plan(m, n, k, true).ksplit);
 }
 

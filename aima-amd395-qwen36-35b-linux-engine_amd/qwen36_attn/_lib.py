@@ -53,8 +53,13 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_gdn_chunk_prefill_workspace_bytes": (_sz, [_u32]),
     "qwen36_gdn_chunk_prefill": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
                                         _vp, _vp, _vp, _u32, _vp, _sz, _vp]),
+    "qwen36_gdn_chunk_prefill_ex": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp,
+                                           _vp, _vp, _vp, _u32, _u32, _vp, _sz, _vp]),
     "qwen36_gdn_fused_gating_update": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32, _u32,
                                               _vp, _u32, _vp, _vp, _vp, _u32, _f32, _u32, _vp]),
+    "qwen36_gdn_fused_gating_update_varlen": (_i32, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _u32,
+                                                     _u32, _vp, _u32, _vp, _vp, _vp, _u32, _vp,
+                                                     _vp, _u32, _u32, _f32, _u32, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     # prefill projections
     "qwen36_prefill_gemm_bf16": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),

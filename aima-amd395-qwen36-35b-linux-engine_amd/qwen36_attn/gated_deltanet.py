@@ -144,6 +144,51 @@ def chunk_gated_delta_rule(query, key, value, g, beta, initial_state=None, chunk
     return out, final_state.view(1, HV, DK, DV)
 
 
+QK_NORMALIZED, STATE_VK = 1, 2   # qwen36_gdn_chunk_prefill_ex flags
+
+
+def vllm_chunk_gated_delta_rule(q, k, v, g, beta, scale: float | None = None,
+                                initial_state: torch.Tensor | None = None,
+                                output_final_state: bool = False,
+                                cu_seqlens=None, head_first: bool = False,
+                                use_qk_l2norm_in_kernel: bool = False):
+    """Mirror of vLLM's ``chunk_gated_delta_rule`` as the reference calls it
+    (fle:6474-6483): q, k [1, T, 16, 128] (unrepeated key heads; v-head h
+    reads key head h // 2), v [1, T, 32, 128] bf16, g (log decay), beta
+    [1, T, 32] fp32, ``initial_state`` [1, 32, 128 (v), 128 (k)] fp32 -- vLLM's
+    orientation, the transpose of the torch path's (handoff fle:5482-5502) --
+    or None for zeros.  ``use_qk_l2norm_in_kernel=False`` (the reference's
+    choice, since fused_post_conv_prep has already normalised q and k) uses
+    q and k as given; True normalises them in the kernel.  Returns (o [1, T,
+    32, 128] bf16, final_state [1, 32, 128, 128] fp32 in the same [v, k]
+    orientation, or None unless ``output_final_state``).  Chunk 64, scale
+    1/sqrt(128) (vLLM's default; other scales are rejected), batch 1 without
+    varlen packing, as the reference uses it."""
+    if cu_seqlens is not None:
+        raise NotImplementedError("cu_seqlens (varlen batches) is not provided: the engine "
+                                  "runs batch 1")
+    if head_first:
+        raise ValueError("head_first layout is not supported (vLLM deprecated it)")
+    if scale is not None and abs(scale - DK ** -0.5) > 1e-12:
+        raise ValueError("the HIP kernel applies scale 1/sqrt(128)")
+    qq, kk, vv, t, hq = _qkv_views(q, k, v)
+    g, beta = _gb(g, beta, t)
+    s_in = None
+    if initial_state is not None:
+        s_in = initial_state.reshape(HV, DV, DK)
+        require(s_in, "initial_state", torch.float32)
+    final_state = torch.empty(HV, DV, DK, dtype=torch.float32, device=qq.device)
+    out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=qq.device)
+    flags = STATE_VK | (0 if use_qk_l2norm_in_kernel else QK_NORMALIZED)
+    lib = _lib.load(("qwen36_gdn_chunk_prefill_ex",))
+    nb = lib.qwen36_gdn_chunk_prefill_workspace_bytes(t)
+    ws = scratch("gdn_chunk", nb, qq.device)
+    _lib.call("qwen36_gdn_chunk_prefill_ex", ptr(qq), ptr(kk), ptr(vv), hq, qq.stride(0),
+              vv.stride(0), ptr(g), ptr(beta), ptr(s_in), ptr(final_state), ptr(out), t,
+              flags, ptr(ws), ws.numel(), stream_handle(qq.device))
+    return out, (final_state.view(1, HV, DV, DK) if output_final_state else None)
+
+
 def gated_rmsnorm(core: torch.Tensor, z: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """fle:6531-6541: rmsnorm_128(core) * w -> bf16 -> * SiLU(z) -> bf16.
     core [T,32,128] (or [1,T,32,128]) bf16, z [T,4096]; returns [T, 4096]."""
@@ -289,34 +334,7 @@ class LinearAttentionLayer:
         return linear(gated, w["out_proj"])
 
 
-def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: float = 1.0,
-                                           threshold: float = 20.0, scale: float | None = None,
-                                           initial_state: torch.Tensor | None = None,
-                                           inplace_final_state: bool = True,
-                                           cu_seqlens=None, ssm_state_indices=None,
-                                           num_accepted_tokens=None,
-                                           use_qk_l2norm_in_kernel: bool = False):
-    """Drop-in for vLLM's ``fused_sigmoid_gating_delta_rule_update`` as the
-    reference's decode calls it (four_layer_mini_engine.py:6429-6440): one
-    sequence, gating fused into the recurrent update, state in vLLM's
-    [Hv, dv, dk] orientation (``qwen36_gdn_fused_gating_update``).
-
-    q, k [1, T, 16 (or 32), 128] bf16; v [1, T, 32, 128] bf16; a, b [T, 32]
-    (or [1, T, 32]) bf16; A_log, dt_bias [32]; initial_state [1, 32, 128, 128]
-    fp32.  Returns (o [1, T, 32, 128] bf16, final_state [1, 32, 128, 128]
-    fp32): the updated ``initial_state`` itself when ``inplace_final_state``,
-    else a new tensor.  Only the single-sequence form is provided: the
-    batching arguments (cu_seqlens, ssm_state_indices, num_accepted_tokens)
-    must be None, and beta/threshold keep vLLM's defaults (1.0, 20.0)."""
-    if cu_seqlens is not None or ssm_state_indices is not None or num_accepted_tokens is not None:
-        raise NotImplementedError("only the single-sequence form is provided")
-    if beta != 1.0 or threshold != 20.0:
-        raise NotImplementedError("softplus beta/threshold other than 1.0/20.0")
-    if initial_state is None:
-        raise ValueError("initial_state is required")
-    qv, kv_, vv, t, hq = _qkv_views(q, k, v)
-    if qv.stride(0) % 8 or vv.stride(0) != HV * DV:
-        raise ValueError("q/k token stride must be a multiple of 8; v must be contiguous")
+def _ab_views(a, b, t):
     a2 = a.reshape(t, HV) if a.dim() == 3 else a
     b2 = b.reshape(t, HV) if b.dim() == 3 else b
     for name, x in (("a", a2), ("b", b2)):
@@ -325,16 +343,122 @@ def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: 
             raise ValueError(f"{name} must be [T, 32]")
     if a2.stride(0) != b2.stride(0):
         raise ValueError("a and b must share a row stride")
-    s_in = initial_state.reshape(HV, DV, DK)
-    require(s_in, "initial_state", torch.float32)
-    final = s_in if inplace_final_state else torch.empty_like(s_in)
+    return a2, b2
+
+
+def _int32_vector(x, name, n, device):
+    if not isinstance(x, torch.Tensor):
+        x = torch.as_tensor(x)
+    x = x.reshape(-1)
+    if x.numel() != n:
+        raise ValueError(f"{name} must hold {n} entries (got {x.numel()})")
+    if x.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{name} must be an integer tensor")
+    return x.to(device=device, dtype=torch.int32).contiguous()
+
+
+def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: float = 1.0,
+                                           threshold: float = 20.0, scale: float | None = None,
+                                           initial_state: torch.Tensor | None = None,
+                                           inplace_final_state: bool = True,
+                                           cu_seqlens=None, ssm_state_indices=None,
+                                           num_accepted_tokens=None,
+                                           use_qk_l2norm_in_kernel: bool = False):
+    """Drop-in for vLLM's ``fused_sigmoid_gating_delta_rule_update`` as the
+    reference's decode calls it (four_layer_mini_engine.py:6429-6440): gating
+    fused into the recurrent update, state in vLLM's [Hv, dv, dk] orientation
+    (``qwen36_gdn_fused_gating_update``).
+
+    q, k [1, T, 16 (or 32), 128] bf16; v [1, T, 32, 128] bf16; a, b [T, 32]
+    (or [1, T, 32]) bf16; A_log, dt_bias [32].  One sequence: initial_state
+    [1, 32, 128, 128] fp32.  Batched (vLLM's varlen form): ``cu_seqlens``
+    [N + 1] token offsets of N sequences, each carrying state slot
+    ``ssm_state_indices[n]`` (default n) of the pool ``initial_state``
+    [slots, 32, 128, 128]; a slot index outside [0, slots) marks a padding
+    sequence, skipped (``qwen36_gdn_fused_gating_update_varlen``).  Returns
+    (o [1, T, 32, 128] bf16, final_state): ``initial_state`` itself, updated,
+    when ``inplace_final_state``, else an updated copy.  num_accepted_tokens
+    (speculative decoding) is not provided; beta/threshold keep vLLM's
+    defaults (1.0, 20.0)."""
+    if num_accepted_tokens is not None:
+        raise NotImplementedError("num_accepted_tokens (speculative decoding) is not provided")
+    if beta != 1.0 or threshold != 20.0:
+        raise NotImplementedError("softplus beta/threshold other than 1.0/20.0")
+    if initial_state is None:
+        raise ValueError("initial_state is required")
+    qv, kv_, vv, t, hq = _qkv_views(q, k, v)
+    if qv.stride(0) % 8:
+        raise ValueError("q/k token stride must be a multiple of 8")
+    a2, b2 = _ab_views(a, b, t)
+    require(initial_state, "initial_state", torch.float32)
+    if initial_state.dim() != 4 or tuple(initial_state.shape[1:]) != (HV, DV, DK):
+        raise ValueError("initial_state must be [slots, 32, 128, 128]")
+    slots = initial_state.shape[0]
+    final = initial_state if inplace_final_state else initial_state.clone()
     out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=qv.device)
     a_log = A_log.float().contiguous()
     dtb = dt_bias.float().contiguous()
     if scale is None:
         scale = DK ** -0.5
-    _lib.call("qwen36_gdn_fused_gating_update", ptr(a_log), ptr(a2), ptr(b2), a2.stride(0),
-              ptr(dtb), ptr(qv), ptr(kv_), hq, qv.stride(0), ptr(vv), vv.stride(0), ptr(s_in),
-              ptr(final), ptr(out), t, float(scale), 1 if use_qk_l2norm_in_kernel else 0,
-              stream_handle(qv.device))
-    return out, (initial_state if inplace_final_state else final.view(1, HV, DV, DK))
+    flags = 1 if use_qk_l2norm_in_kernel else 0
+    if cu_seqlens is None and ssm_state_indices is None:
+        if slots != 1:
+            raise ValueError("a single sequence takes a [1, 32, 128, 128] state")
+        _lib.call("qwen36_gdn_fused_gating_update", ptr(a_log), ptr(a2), ptr(b2), a2.stride(0),
+                  ptr(dtb), ptr(qv), ptr(kv_), hq, qv.stride(0), ptr(vv), vv.stride(0),
+                  ptr(initial_state), ptr(final), ptr(out), t, float(scale), flags,
+                  stream_handle(qv.device))
+        return out, final
+    if cu_seqlens is None:
+        cu_seqlens = torch.tensor([0, t], dtype=torch.int32)
+    n = (cu_seqlens.numel() if isinstance(cu_seqlens, torch.Tensor) else len(cu_seqlens)) - 1
+    cu = _int32_vector(cu_seqlens, "cu_seqlens", n + 1, qv.device)
+    idx = None
+    if ssm_state_indices is not None:
+        idx = _int32_vector(ssm_state_indices, "ssm_state_indices", n, qv.device)
+    _lib.call("qwen36_gdn_fused_gating_update_varlen", ptr(a_log), ptr(a2), ptr(b2),
+              a2.stride(0), ptr(dtb), ptr(qv), ptr(kv_), hq, qv.stride(0), ptr(vv), vv.stride(0),
+              ptr(initial_state), ptr(final), ptr(out), t, ptr(cu), ptr(idx), n, slots,
+              float(scale), flags, stream_handle(qv.device))
+    return out, final
+
+
+def fused_recurrent_gated_delta_rule_packed_decode(mixed_qkv, a, b, A_log, dt_bias, scale,
+                                                   initial_state, out=None,
+                                                   ssm_state_indices=None,
+                                                   use_qk_l2norm_in_kernel: bool = True):
+    """Mirror of vLLM's packed decode as the reference calls it
+    (``vllm_fused_recurrent_gdn_packed_decode``, fle:6396-6417): B decode
+    tokens, each its own sequence, read straight from the conv output
+    ``mixed_qkv`` [B, 8192] bf16 (q | k | v columns); a, b [B, 32] bf16;
+    token n updates slot ``ssm_state_indices[n]`` (default n) of the pool
+    ``initial_state`` [slots, 32, 128 (v), 128 (k)] fp32 in place (slots
+    outside [0, slots) are padding, skipped).  Returns (out [B, 1, 32, 128]
+    bf16, initial_state).  ``out`` may be given (same shape, bf16)."""
+    require(mixed_qkv, "mixed_qkv", torch.bfloat16, contiguous=False)
+    if mixed_qkv.dim() != 2 or mixed_qkv.shape[1] != CONV_DIM or mixed_qkv.stride(1) != 1:
+        raise ValueError("mixed_qkv must be [B, 8192] with unit inner stride")
+    n = mixed_qkv.shape[0]
+    if mixed_qkv.stride(0) % 8 or mixed_qkv.data_ptr() % 16:
+        raise ValueError("mixed_qkv rows must be 16-byte aligned")
+    a2, b2 = _ab_views(a, b, n)
+    require(initial_state, "initial_state", torch.float32)
+    if initial_state.dim() != 4 or tuple(initial_state.shape[1:]) != (HV, DV, DK):
+        raise ValueError("initial_state must be [slots, 32, 128, 128]")
+    if out is None:
+        out = torch.empty(n, 1, HV, DV, dtype=torch.bfloat16, device=mixed_qkv.device)
+    require(out, "out", torch.bfloat16)
+    if out.numel() != n * HV * DV:
+        raise ValueError("out must hold [B, 1, 32, 128]")
+    idx = None
+    if ssm_state_indices is not None:
+        idx = _int32_vector(ssm_state_indices, "ssm_state_indices", n, mixed_qkv.device)
+    base = mixed_qkv.data_ptr()
+    a_log = A_log.float().contiguous()
+    dtb = dt_bias.float().contiguous()
+    _lib.call("qwen36_gdn_fused_gating_update_varlen", ptr(a_log), ptr(a2), ptr(b2),
+              a2.stride(0), ptr(dtb), base, base + 2 * KEY_DIM, HK, mixed_qkv.stride(0),
+              base + 2 * 2 * KEY_DIM, mixed_qkv.stride(0), ptr(initial_state), ptr(initial_state),
+              ptr(out), n, None, ptr(idx), n, initial_state.shape[0], float(scale),
+              1 if use_qk_l2norm_in_kernel else 0, stream_handle(mixed_qkv.device))
+    return out, initial_state

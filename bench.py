@@ -471,6 +471,37 @@ def bench_gdn_recurrent(torch, dev, layers, iters, warmup, use_graph, seed=2):
             "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_gdn_fused_gating_update(torch, dev, layers, iters, warmup, use_graph, seed=5):
+    """vLLM-orientation decode update (gating fused, [Hv, dv, dk] state,
+    qwen36_gdn_fused_gating_update) for one token through 30 layers with their
+    own states updated in place -- the same state traffic as
+    bench_gdn_recurrent, in the orientation the reference's decode keeps."""
+    from qwen36_attn import _lib
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(seed)
+    mixed = [syn.randn((1, 8192), g).to(dev) for _ in range(layers)]
+    ab = [syn.randn((1, 64), g).to(dev) for _ in range(layers)]
+    a_log = torch.log(torch.rand(32, generator=g) * 16 + 1e-4).float().to(dev)
+    dtb = torch.randn(32, generator=g).float().to(dev)
+    states = [(torch.randn(32, 128, 128, generator=g) * 0.2).to(dev) for _ in range(layers)]
+    outs = [torch.empty(1, 32, 128, dtype=torch.bfloat16, device=dev) for _ in range(layers)]
+
+    def step():
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(layers):
+            base = mixed[i].data_ptr()
+            _lib.call("qwen36_gdn_fused_gating_update", a_log.data_ptr(), ab[i].data_ptr(),
+                      ab[i].data_ptr() + 64, 64, dtb.data_ptr(), base, base + 4096, 16, 8192,
+                      base + 8192, 8192, states[i].data_ptr(), states[i].data_ptr(),
+                      outs[i].data_ptr(), 1, 128 ** -0.5, 1, st)
+    run = make_graph(torch, step).replay if use_graph else step
+    ms = Timer(torch).time(run, iters, warmup)
+    us = ms * 1000.0
+    nbytes = GDN_STATE_BYTES * layers
+    return {"layers": layers, "us_per_token": us, "hbm_gbs": nbytes / (us * 1e-6) / 1e9,
+            "frac_hbm": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def bench_gdn_decode_step(torch, dev, layers, iters, warmup, use_graph, fused=True, seed=4):
     """Everything between a GDN layer's input projections and out_proj for
     one decode token (conv, gating, l2norm, recurrent delta rule, gated
@@ -545,6 +576,75 @@ def bench_config1_layers(torch, dev, t, iters, warmup, seed=12):
     del fl, ll, wf, wl
     torch.cuda.empty_cache()
     return res
+
+
+def _config1_sequence(layer_fn, x, steps):
+    """Config 1's sequence: a causal prefill of the prompt, then ``steps``
+    decode steps, each feeding the layer's own last output row back as the
+    next input (a single layer has no greedy token to embed)."""
+    out = layer_fn(x, 0, "prefill")
+    t = x.shape[0]
+    for i in range(steps):
+        out = layer_fn(out[-1:].contiguous(), t + i, "decode")
+    return out
+
+
+def bench_config1_sequence(torch, dev, t=1024, steps=16, iters=10, warmup=2, seed=21):
+    """Config 1 exactly as BASELINE defines it, on the GPU: one gated
+    full-attention layer (random N(0, 0.02) weights, x ~ N(0,1)*0.5), a
+    1,024-token causal prefill then 16 decode steps appending to the KV
+    cache; wall time of the whole sequence (eager launches)."""
+    from qwen36_attn import synthetic as syn
+    from qwen36_attn.full_attention import FullAttentionLayer
+    g = syn.gen(seed)
+    wf = {k: v.to(dev) for k, v in syn.full_attention_weights(g).items()}
+    fl = FullAttentionLayer(wf, t + steps + 64, dev)
+    x = syn.randn((t, 2048), g, 0.5).to(dev)
+    tm = Timer(torch)
+    ms = tm.time(lambda: _config1_sequence(fl.forward, x, steps), iters, warmup)
+    del fl, wf
+    torch.cuda.empty_cache()
+    return {"tokens": t, "decode_steps": steps, "ms": ms}
+
+
+def cpu_config1_baseline(torch, t=1024, steps=16, seed=21):
+    """Config 1 on this host's cores, the reference's CPU plumbing path: the
+    oracle's gated full-attention layer (torch CPU, bf16 weights and
+    activations as fle:6546-6653) over the same sequence as
+    bench_config1_sequence; median of at least 3 whole sequences."""
+    from oracle import attention_oracle as O
+    from qwen36_attn import synthetic as syn
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = syn.gen(seed)
+    w = syn.full_attention_weights(g)
+    x = syn.randn((t, 2048), g, 0.5)
+    k_cache = torch.zeros(t + steps, 2, 256, dtype=torch.bfloat16)
+    v_cache = torch.zeros_like(k_cache)
+    fn = lambda inp, pos, mode: O.full_attention(inp, w, k_cache, v_cache, pos, mode)
+    med, n = _median_time(lambda: _config1_sequence(fn, x, steps), min_runs=3, budget_s=20.0)
+    return {"value": med * 1e3, "unit": "ms", "cores": threads, "kind": "port",
+            "sample": f"median of {n} whole config-1 sequences ({t}-token prefill + {steps} "
+                      f"decode steps, one layer) through the oracle (torch CPU, {_cpu_info()})"}
+
+
+def cpu_decode_32k_baseline(torch, cache_end=32768):
+    """Config 2 on this host's cores: the oracle's grouped bf16 decode of one
+    layer at S = 32768, median of at least 3; and x10 for the model's 10
+    full-attention layers."""
+    from oracle import attention_oracle as O
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(8)
+    k = torch.randn(cache_end, 2, 256, generator=gen).to(torch.bfloat16)
+    v = torch.randn(cache_end, 2, 256, generator=gen).to(torch.bfloat16)
+    q = torch.randn(1, 16, 256, generator=gen).to(torch.bfloat16)
+    med, n = _median_time(lambda: O.decode_attention_grouped_bf16(q, k, v, cache_end),
+                          min_runs=5, budget_s=5.0, max_runs=50)
+    return {"us_per_layer": med * 1e6, "us_10layers": med * 1e6 * N_FULL_LAYERS,
+            "cores": threads, "kind": "port",
+            "sample": f"median of {n} single-layer grouped-bf16 decodes at S={cache_end} "
+                      f"(oracle, torch CPU, {_cpu_info()})"}
 
 
 def bench_gdn_prefill(torch, dev, t, iters, warmup, seed=3):
@@ -689,6 +789,7 @@ def run_only(torch, fa, dev, args):
         r = bench_prefill_projections(torch, dev, 8192, args.steps, args.warmup)
     elif args.only == "gdn":
         r = [bench_gdn_recurrent(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
+             bench_gdn_fused_gating_update(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
     elif args.only == "moe":
@@ -736,6 +837,8 @@ def main():
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
+        "gdn_fused_gating_update_30layers": bench_gdn_fused_gating_update(torch, dev, GDN_LAYERS,
+                                                                          50, 5, use_graph),
         "prefix_cache_32k": bench_prefix_cache(torch, dev, 32768, 20, 3),
         "decode_projections_40layers": bench_decode_projections(torch, dev, 20, 3, use_graph),
         "moe_decode_40layers": bench_moe_decode(torch, dev, 40, 20, 3, use_graph),
@@ -746,6 +849,7 @@ def main():
                                                              use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
         "config1_layers_1k": bench_config1_layers(torch, dev, 1024, 20, 3),
+        "config1_sequence": bench_config1_sequence(torch, dev),
         "prefill_projections_1k": bench_prefill_projections(torch, dev, 1024, 20, 3),
         "prefill_projections_1k_torch": bench_prefill_projections(torch, dev, 1024, 20, 3,
                                                                   native=False),
@@ -771,6 +875,8 @@ def main():
     if not args.no_cpu:
         extra["cpu_prefill_config3"] = cpu_prefill_baseline(torch)
         extra["cpu_gdn_config4"] = cpu_gdn_baseline(torch)
+        extra["cpu_config1"] = cpu_config1_baseline(torch)
+        extra["cpu_decode_config2"] = cpu_decode_32k_baseline(torch)
     line = {
         "metric": "decode attn us/tok + HBM GB/s @128K ctx; prefill attn TFLOP/s @8K tokens",
         "value": head["us_per_token"], "unit": "us/token", "n_gpus": 1,

@@ -180,7 +180,16 @@ int qwen36_output_gate(const void* attn, int attn_is_f32, const void* q_gate,
  *   (:5167-5240, chunk 64) / the FLA chunk pipeline launched by
  *   native_linear_prefill.hip.cpp:474-836.  Same tensors as the recurrent
  *   step; state_in may be NULL (zeros).  Workspace of at least
- *   qwen36_gdn_chunk_prefill_workspace_bytes(tokens) bytes.
+ *   qwen36_gdn_chunk_prefill_workspace_bytes(tokens) bytes.  q, k and v
+ *   16-byte aligned (their rows are read as 16-byte vectors).
+ * qwen36_gdn_chunk_prefill_ex: the same with flags, for vLLM's
+ *   chunk_gated_delta_rule(q, k, v, g, beta, initial_state,
+ *   output_final_state, use_qk_l2norm_in_kernel) as the reference calls it
+ *   (four_layer_mini_engine.py:6474-6483, state handoff :5482-5502):
+ *   QWEN36_GDN_QK_NORMALIZED = use_qk_l2norm_in_kernel=False (q and k arrive
+ *   l2-normalised and are used as given); QWEN36_GDN_STATE_VK = state_in and
+ *   state_out in vLLM's [32, 128 (v), 128 (k)] orientation.  Flags 0 is
+ *   qwen36_gdn_chunk_prefill.  Unknown flag bits are rejected.
  * qwen36_gdn_gated_norm: replaces linear_gated_norm_fused_kernel
  *   (native_pointwise.hip.cpp:376-430; :6531-6541): core [T,32,128],
  *   z [T, >=4096 stride], weight [128] bf16 -> out [T,4096]. */
@@ -205,6 +214,15 @@ int qwen36_gdn_chunk_prefill(const void* q, const void* k, const void* v,
                              void* state_out, void* out, unsigned tokens,
                              void* workspace, size_t workspace_bytes,
                              void* stream);
+#define QWEN36_GDN_QK_NORMALIZED 1u
+#define QWEN36_GDN_STATE_VK 2u
+int qwen36_gdn_chunk_prefill_ex(const void* q, const void* k, const void* v,
+                                unsigned qk_heads, unsigned qk_token_stride,
+                                unsigned v_token_stride, const void* g,
+                                const void* beta, const void* state_in,
+                                void* state_out, void* out, unsigned tokens,
+                                unsigned flags, void* workspace,
+                                size_t workspace_bytes, void* stream);
 int qwen36_gdn_gated_norm(const void* core, const void* z,
                           unsigned z_row_stride, const void* weight, void* out,
                           unsigned tokens, void* stream);
@@ -228,6 +246,26 @@ int qwen36_gdn_fused_gating_update(const void* a_log, const void* a, const void*
                                    unsigned v_token_stride, const void* state_in,
                                    void* state_out, void* out, unsigned tokens,
                                    float scale, unsigned flags, void* stream);
+/* qwen36_gdn_fused_gating_update_varlen: the same update over N sequences,
+ *   for vLLM's batched calls -- fused_sigmoid_gating_delta_rule_update with
+ *   cu_seqlens / ssm_state_indices, and the packed decode
+ *   fused_recurrent_gated_delta_rule_packed_decode
+ *   (four_layer_mini_engine.py:6396-6417).  Sequence n covers tokens
+ *   [cu_seqlens[n], cu_seqlens[n+1]) (int32 [N+1]; NULL: token n alone, then
+ *   N == tokens) and carries state slot state_indices[n] (int32 [N]; NULL:
+ *   slot n) of the pools state_in -> state_out [n_slots, 32, 128 (v), 128 (k)]
+ *   fp32 (may alias).  A slot outside [0, n_slots), or an empty sequence, is
+ *   padding: skipped, its outputs and state slot untouched.  1 <= N <= 65535;
+ *   other arguments as qwen36_gdn_fused_gating_update. */
+int qwen36_gdn_fused_gating_update_varlen(const void* a_log, const void* a, const void* b,
+                                          unsigned ab_row_stride, const void* dt_bias,
+                                          const void* q, const void* k, unsigned qk_heads,
+                                          unsigned qk_token_stride, const void* v,
+                                          unsigned v_token_stride, const void* state_in,
+                                          void* state_out, void* out, unsigned tokens,
+                                          const void* cu_seqlens, const void* state_indices,
+                                          unsigned n_seqs, unsigned n_slots, float scale,
+                                          unsigned flags, void* stream);
 
 /* qwen36_gdn_decode_step: one launch for everything between the GDN input
  *   projections and out_proj -- conv1d + SiLU, gating, l2norm, the recurrent
@@ -273,7 +311,8 @@ int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y
  * once, so the result is deterministic; it can differ from
  * qwen36_prefill_gemm_bf16's by the fp32 summation order (well inside one
  * bf16 rounding).  workspace_bytes returns 0 when the shape runs unsplit (ws
- * may then be NULL); otherwise ws is 16-byte aligned and holds at least that
+ * may then be NULL) and for a shape the launch rejects (m, n or k out of the
+ * ranges above); otherwise ws is 16-byte aligned and holds at least that
  * many bytes, else the call returns the invalid-argument code.  Same
  * reference call sites as qwen36_prefill_gemm_bf16. */
 size_t qwen36_prefill_gemm_workspace_bytes(unsigned m, unsigned n, unsigned k);

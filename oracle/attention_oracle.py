@@ -229,16 +229,19 @@ def repeat_kv_heads(x: torch.Tensor) -> torch.Tensor:
     return x.repeat_interleave(GDN_HV // GDN_HK, dim=1)
 
 
-def chunk_gated_delta_rule(query, key, value, g, beta, initial_state, chunk_size: int = 64):
+def chunk_gated_delta_rule(query, key, value, g, beta, initial_state, chunk_size: int = 64,
+                           qk_l2norm: bool = True):
     """fle:5167-5240 ``torch_chunk_gated_delta_rule``.
 
     query/key [B,T,H,dk], value [B,T,H,dv] (any float dtype; heads already
     repeated to Hv), g/beta [B,T,H] fp32, initial_state [B,H,dk,dv] fp32.
     Returns (out [B,T,H,dv] bf16, final_state [B,H,dk,dv] fp32).  All
     arithmetic is fp32; the chunk loop is the WY/UT form with the forward
-    substitution of fle:5207-5211."""
-    query = l2norm(query)
-    key = l2norm(key)
+    substitution of fle:5207-5211.  ``qk_l2norm=False`` skips the l2norm of
+    q and k (used by the vLLM form below)."""
+    if qk_l2norm:
+        query = l2norm(query)
+        key = l2norm(key)
     query, key, value, beta, g = [x.transpose(1, 2).contiguous().to(torch.float32)
                                   for x in (query, key, value, beta, g)]
     bsz, nh, seq, dk = key.shape
@@ -281,6 +284,31 @@ def chunk_gated_delta_rule(query, key, value, g, beta, initial_state, chunk_size
                  + (k_c * (g_last[..., None] - g[:, :, c]).exp()[..., None]).transpose(-1, -2) @ v_new)
     out = out.reshape(bsz, nh, -1, dv)[:, :, :seq]
     return out.transpose(1, 2).contiguous().to(DTYPE), state
+
+
+def vllm_chunk_gated_delta_rule(q, k, v, g, beta, initial_state,
+                                use_qk_l2norm_in_kernel: bool = False):
+    """vLLM's ``chunk_gated_delta_rule`` as the reference calls it
+    (fle:6474-6483; vLLM 0.19.1rc1.dev300+g29e5d1020, third-party code not
+    under the reference tree).  Its published algorithm is the gated delta
+    rule of torch_chunk_gated_delta_rule (fle:5167-5240) with three interface
+    differences: q, k carry the 16 key heads (v-head j reads key head
+    j // 2), the state is stored [Hv, dv, dk] (the transpose; the reference
+    hands states over with ``.transpose(-1, -2)``, fle:5482-5502), and q, k are
+    l2-normalised in the kernel only when ``use_qk_l2norm_in_kernel`` (the
+    reference passes False: fused_post_conv_prep normalised them already).
+    q, k [1,T,16,dk], v [1,T,32,dv], g/beta [1,T,32], initial_state
+    [1,32,dv,dk] fp32 or None -> (o [1,T,32,dv] bf16, final_state
+    [1,32,dv,dk] fp32)."""
+    rep = v.shape[2] // q.shape[2]
+    qq = q.repeat_interleave(rep, dim=2)
+    kk = k.repeat_interleave(rep, dim=2)
+    if initial_state is None:
+        s0 = torch.zeros(1, v.shape[2], q.shape[-1], v.shape[-1])
+    else:
+        s0 = initial_state.float().transpose(-1, -2)
+    o, s = chunk_gated_delta_rule(qq, kk, v, g, beta, s0, qk_l2norm=use_qk_l2norm_in_kernel)
+    return o, s.transpose(-1, -2).contiguous()
 
 
 def recurrent_gated_delta_rule(query, key, value, g, beta, initial_state):

@@ -80,6 +80,23 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qwen36_decode_gqa_workspace_bytes(131072, 0) > 0
     assert L.qwen36_gdn_recurrent(1, 1, 1, 8, 2048, 4096, 1, 1, 1, 1, 1, 1, None) == 1  # qk_heads
     assert L.qwen36_gdn_chunk_prefill(1, 1, 1, 16, 2048, 4096, 1, 1, None, 1, 1, 64, 1, 0, None) == 1
+    # chunk prefill: q / k / v base pointers not 16-byte aligned, unknown flags
+    big = 1 << 30
+    assert L.qwen36_gdn_chunk_prefill(24, 16, 16, 16, 2048, 4096, 16, 16, None, 16, 16, 64, 16,
+                                      big, None) == 1
+    assert L.qwen36_gdn_chunk_prefill(16, 16, 8, 16, 2048, 4096, 16, 16, None, 16, 16, 64, 16,
+                                      big, None) == 1
+    cpx = L.qwen36_gdn_chunk_prefill_ex
+    assert cpx(16, 16, 16, 16, 2048, 4096, 16, 16, None, 16, 16, 64, 4, 16, big, None) == 1
+    assert cpx(16, 24, 16, 16, 2048, 4096, 16, 16, None, 16, 16, 64, 3, 16, big, None) == 1
+    # varlen gating update: no cu_seqlens needs one sequence per token; zero
+    # sequences or slots; more than 65535 sequences
+    fv = L.qwen36_gdn_fused_gating_update_varlen
+    base = (16, 16, 16, 32, 16, 16, 16, 16, 2048, 16, 4096, 16, 16, 16)
+    assert fv(*base, 4, None, None, 3, 4, 0.088, 1, None) == 1
+    assert fv(*base, 4, 16, None, 0, 4, 0.088, 1, None) == 1
+    assert fv(*base, 4, 16, None, 2, 0, 0.088, 1, None) == 1
+    assert fv(*base, 4, 16, None, 65536, 4, 0.088, 1, None) == 1
     assert L.qwen36_gdn_conv1d(1, 100, 1, 1, 1, 1, 4, None) == 1  # row stride < 8192
     assert L.qwen36_head_norm_rope(1, 8192, 1, 512, 1, 512, 1, 1, 0, 0, 1, 1, 1, None) == 1
     assert L.qwen36_output_gate(1, 0, 1, 100, 1, 1, None) == 1
@@ -133,8 +150,27 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert G(1024, 2048, 4096) == 2 * 1024 * 2048 * 4
     assert G(256, 2048, 4096) % (256 * 2048 * 4) == 0 and G(256, 2048, 4096) > 0
     assert G(1024, 2048, 4000) == 0 and G(0, 2048, 4096) == 0
+    # shapes the launch rejects size no workspace
+    assert G(1024, 2048, 16384 + 64) == 0 and G(1024, 65537, 4096) == 0
+    assert G(262145, 2048, 4096) == 0
     assert L.qwen36_prefill_gemm_bf16_ws(16, 2048, 16, 16, 2048, 300, 2048, 4096,
                                          16, G(300, 2048, 4096) - 16, None) == 1
+
+
+def test_scratch_growth_is_geometric_and_bounded():
+    """Workspaces that grow with the prompt keep their outgrown buffers (a
+    captured graph may hold them), so growth must be geometric: after rising
+    requests the dead buffers of a tag stay below its live buffer."""
+    from qwen36_attn import _tensors as T
+    dev = torch.device("cpu")
+    tag = "growth_test"
+    for n in range(64, 8193, 64):
+        buf = T.scratch(tag, n * 1000, dev)
+        assert buf.numel() >= n * 1000
+    live = T._SCRATCH[(tag, 0)].numel()
+    assert live & (live - 1) == 0            # a power of two
+    assert T.retired_bytes(tag) < live
+    assert T.scratch(tag, 100, dev).numel() == live   # smaller requests reuse it
 
 
 def test_prefix_cache_host_bookkeeping_without_device(lib):

@@ -7,7 +7,10 @@ them, against the oracle on identical seeded inputs:
     states, position window, mode);
   * vLLM's fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k,
     v, initial_state, inplace_final_state, use_qk_l2norm_in_kernel)
-    (fle:6429-6440) with the [Hv, dv, dk] state.
+    (fle:6429-6440) with the [Hv, dv, dk] state, its batched cu_seqlens /
+    ssm_state_indices form and the packed decode (fle:6396-6417);
+  * vLLM's chunk_gated_delta_rule(q, k, v, g, beta, initial_state,
+    output_final_state, use_qk_l2norm_in_kernel) (fle:6474-6483).
 """
 import pytest
 import torch
@@ -142,3 +145,117 @@ def test_fused_sigmoid_gating_delta_rule_update(gpu, t, norm, inplace):
                                                 h0.transpose(-1, -2))
         assert (ro2.float() - ro.float()).abs().max().item() <= TOL
         assert ((rs2.transpose(-1, -2) - rs).norm() / rs.norm()).item() <= 1e-5
+
+
+@pytest.mark.parametrize("t,norm", [(200, False), (64, True)])
+def test_vllm_chunk_gated_delta_rule(gpu, t, norm):
+    """vLLM's chunk_gated_delta_rule as the reference calls it (fle:6474-6483):
+    16-head q/k, the [1, 32, dv, dk] state handed over transposed
+    (fle:5482-5502), use_qk_l2norm_in_kernel=False on q/k that
+    fused_post_conv_prep already normalised (and True on raw ones)."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(91 + t)
+    q = torch.randn(1, t, 16, 128, generator=g)
+    k = torch.randn(1, t, 16, 128, generator=g)
+    if not norm:
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = syn.randn((1, t, 32, 128), g)
+    beta = torch.sigmoid(torch.randn(1, t, 32, generator=g))
+    gg = -torch.nn.functional.softplus(torch.randn(1, t, 32, generator=g)) * 0.5
+    h0 = torch.randn(1, 32, 128, 128, generator=g) * 0.2      # [Hv, dv, dk]
+    print(f"vllm chunk rule T={t} l2norm_in_kernel={norm}", flush=True)
+    d = lambda x: x.to(gpu)
+    o, fin = G.vllm_chunk_gated_delta_rule(q=d(q), k=d(k), v=d(v), g=d(gg), beta=d(beta),
+                                           initial_state=d(h0), output_final_state=True,
+                                           use_qk_l2norm_in_kernel=norm)
+    ro, rs = O.vllm_chunk_gated_delta_rule(q, k, v, gg, beta, h0, norm)
+    assert o.shape == (1, t, 32, 128) and fin.shape == (1, 32, 128, 128)
+    assert (o.cpu().float() - ro.float()).abs().max().item() <= TOL
+    assert ((fin.cpu() - rs).norm() / rs.norm()).item() <= 1e-3
+    # zero state as None, no final state requested
+    o2, none = G.vllm_chunk_gated_delta_rule(d(q), d(k), d(v), d(gg), d(beta), initial_state=None,
+                                             use_qk_l2norm_in_kernel=norm)
+    ro2, _ = O.vllm_chunk_gated_delta_rule(q, k, v, gg, beta, None, norm)
+    assert none is None
+    assert (o2.cpu().float() - ro2.float()).abs().max().item() <= TOL
+
+
+def _gating_inputs(g, t):
+    a = syn.randn((t, 32), g)
+    b = syn.randn((t, 32), g)
+    a_log = torch.log(torch.rand(32, generator=g) * 8 + 0.05).float()
+    dt = (torch.randn(32, generator=g) * 0.5).float()
+    return a, b, a_log, dt
+
+
+def test_fused_gating_update_varlen_state_indices(gpu):
+    """vLLM's batched form: cu_seqlens [0, 2, 2, 5, 6] (one empty sequence)
+    and ssm_state_indices [3, 0, 1, -1] (the last sequence is padding) over a
+    pool of 4 slots; each sequence equals the single-sequence oracle on its
+    slot, and untouched slots keep their values."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(404)
+    t = 6
+    q = syn.randn((1, t, 16, 128), g)
+    k = syn.randn((1, t, 16, 128), g)
+    v = syn.randn((1, t, 32, 128), g)
+    a, b, a_log, dt = _gating_inputs(g, t)
+    pool = torch.randn(4, 32, 128, 128, generator=g) * 0.2
+    cu = [0, 2, 2, 5, 6]
+    idx = [3, 0, 1, -1]
+    d = lambda x: x.to(gpu)
+    state = d(pool).contiguous()
+    print("fused gating update varlen", flush=True)
+    o, fin = G.fused_sigmoid_gating_delta_rule_update(
+        A_log=d(a_log), a=d(a), b=d(b), dt_bias=d(dt), q=d(q), k=d(k), v=d(v),
+        initial_state=state, inplace_final_state=True,
+        cu_seqlens=torch.tensor(cu, dtype=torch.int64), ssm_state_indices=torch.tensor(idx),
+        use_qk_l2norm_in_kernel=True)
+    assert fin.data_ptr() == state.data_ptr()
+    fin = fin.cpu()
+    o = o.cpu()
+    for n in range(4):
+        t0, t1, sl = cu[n], cu[n + 1], idx[n]
+        if sl < 0 or t1 == t0:
+            continue
+        ro, rs = O.fused_sigmoid_gating_delta_rule_update(
+            a_log, a[t0:t1], b[t0:t1], dt, q[:, t0:t1], k[:, t0:t1], v[:, t0:t1],
+            pool[sl:sl + 1], True)
+        assert (o[:, t0:t1].float() - ro.float()).abs().max().item() <= TOL
+        assert ((fin[sl] - rs[0]).norm() / rs.norm()).item() <= 1e-3
+    assert torch.equal(fin[2], pool[2])   # no sequence uses slot 2
+
+
+def test_packed_decode_from_conv_output(gpu):
+    """vLLM's packed decode as the reference calls it (fle:6396-6417): B
+    tokens read straight from the [B, 8192] conv output, token n updating
+    slot ssm_state_indices[n] in place (-1 = padding)."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(405)
+    bsz = 3
+    mixed = syn.randn((bsz, 8192), g)
+    a, b, a_log, dt = _gating_inputs(g, bsz)
+    pool = torch.randn(3, 32, 128, 128, generator=g) * 0.2
+    idx = [2, 0, -1]
+    d = lambda x: x.to(gpu)
+    state = d(pool).contiguous()
+    print("packed decode", flush=True)
+    out, fin = G.fused_recurrent_gated_delta_rule_packed_decode(
+        mixed_qkv=d(mixed), a=d(a), b=d(b), A_log=d(a_log), dt_bias=d(dt), scale=128 ** -0.5,
+        initial_state=state, ssm_state_indices=d(torch.tensor(idx, dtype=torch.int32)),
+        use_qk_l2norm_in_kernel=True)
+    assert out.shape == (bsz, 1, 32, 128) and fin.data_ptr() == state.data_ptr()
+    out, fin = out.cpu(), fin.cpu()
+    for n in range(bsz):
+        if idx[n] < 0:
+            continue
+        qn = mixed[n, :2048].view(1, 1, 16, 128)
+        kn = mixed[n, 2048:4096].view(1, 1, 16, 128)
+        vn = mixed[n, 4096:].view(1, 1, 32, 128)
+        ro, rs = O.fused_sigmoid_gating_delta_rule_update(
+            a_log, a[n:n + 1], b[n:n + 1], dt, qn, kn, vn, pool[idx[n]:idx[n] + 1], True)
+        assert (out[n].float() - ro[0].float()).abs().max().item() <= TOL
+        assert ((fin[idx[n]] - rs[0]).norm() / rs.norm()).item() <= 1e-3
+    assert torch.equal(fin[1], pool[1])

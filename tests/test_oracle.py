@@ -205,13 +205,16 @@ def test_l2norm_and_gating():
     assert torch.allclose(beta32.double(), exact, rtol=1e-6)
 
 
-def brute_delta_rule(q, k, v, g, beta, s0):
+def brute_delta_rule(q, k, v, g, beta, s0, norm=True):
     """fp64 textbook gated delta rule, token by token, per head.
-    q,k [T,H,dk] (raw), v [T,H,dv], g,beta [T,H], s0 [H,dk,dv]."""
+    q,k [T,H,dk] (raw; l2-normalised here unless ``norm`` is False), v
+    [T,H,dv], g,beta [T,H], s0 [H,dk,dv]."""
     q = q.double()
     k = k.double()
-    q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6) / math.sqrt(q.shape[-1])
-    k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    if norm:
+        q = q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)
+        k = k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    q = q / math.sqrt(q.shape[-1])
     s = s0.double().clone()
     outs = []
     for t in range(q.shape[0]):
@@ -244,6 +247,48 @@ def test_delta_rules_match_brute_force(t):
     for o, s in ((ro, rs), (co, cs)):
         assert (o[0].double() - ref_o).abs().max() <= 2e-2
         assert ((s[0].double() - ref_s).norm() / ref_s.norm()) <= 1e-5
+
+
+def test_vllm_chunk_rule_matches_fp64_brute_force():
+    """Pins oracle.vllm_chunk_gated_delta_rule (vLLM's chunk API, fle:6474-6483):
+    16 key heads read by v-head pairs, the [Hv, dv, dk] state, and q, k used
+    as given without the in-kernel l2norm.  The brute force normalises inside,
+    given the flag off, the brute force without its normalisation must agree;
+    raw inputs must agree with the normalising brute force when the flag is
+    on, and differ from it when it is off."""
+    t = 70
+    g = gen(77)
+    q = torch.randn(t, 16, 128, generator=g)
+    k = torch.randn(t, 16, 128, generator=g)
+    v = torch.randn(t, 32, 128, generator=g).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn(t, 32, generator=g))
+    gg = -F.softplus(torch.randn(t, 32, generator=g)) * 0.5
+    s0 = torch.randn(32, 128, 128, generator=g)          # [Hv, dk, dv]
+    qn = (q / torch.sqrt((q * q).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    kn = (k / torch.sqrt((k * k).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    rep = lambda x: x.repeat_interleave(2, dim=1)
+    ref_o, ref_s = brute_delta_rule(rep(qn), rep(kn), v, gg, beta, s0, norm=False)
+    b = lambda x: x.unsqueeze(0)
+    o, s = O.vllm_chunk_gated_delta_rule(b(qn), b(kn), b(v), b(gg), b(beta),
+                                         b(s0.transpose(-1, -2)), False)
+    assert s.shape == (1, 32, 128, 128)
+    assert (o[0].double() - ref_o).abs().max() <= 2e-2
+    assert ((s[0].transpose(-1, -2).double() - ref_s).norm() / ref_s.norm()) <= 1e-5
+    # raw inputs: the flag decides whether they are normalised
+    qr, kr = (q * 0.1).to(torch.bfloat16), (k * 0.1).to(torch.bfloat16)
+    ref_o2, ref_s2 = brute_delta_rule(rep(qr), rep(kr), v, gg, beta, s0)
+    o_on, s_on = O.vllm_chunk_gated_delta_rule(b(qr), b(kr), b(v), b(gg), b(beta),
+                                               b(s0.transpose(-1, -2)), True)
+    o_off, s_off = O.vllm_chunk_gated_delta_rule(b(qr), b(kr), b(v), b(gg), b(beta),
+                                                 b(s0.transpose(-1, -2)), False)
+    assert (o_on[0].double() - ref_o2).abs().max() <= 2e-2
+    assert ((s_off[0].transpose(-1, -2).double() - ref_s2).norm() / ref_s2.norm()) > 1e-2
+    # zero initial state given as None
+    oz, sz = O.vllm_chunk_gated_delta_rule(b(qn), b(kn), b(v), b(gg), b(beta), None, False)
+    ref_oz, ref_sz = brute_delta_rule(rep(qn), rep(kn), v, gg, beta, torch.zeros(32, 128, 128),
+                                      norm=False)
+    assert (oz[0].double() - ref_oz).abs().max() <= 2e-2
+    assert ((sz[0].transpose(-1, -2).double() - ref_sz).norm() / ref_sz.norm()) <= 1e-5
 
 
 def test_chunk_size_invariance_and_carry():
