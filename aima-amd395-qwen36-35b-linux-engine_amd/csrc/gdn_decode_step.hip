@@ -60,18 +60,21 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
 
   // ---- conv channel owned by this thread (threads 0..383) ----------------
   // local 0..127: q of key head kh; 128..255: k of key head kh; 256..383: v.
+  // Threads 384.. own no channel and read channel 0's inputs (unused), so
+  // every load below is unconditional: all of a token's inputs and the state
+  // are requested before any is used (one memory round trip; loads inside
+  // divergent branches made the compiler wait at each branch's end).
   const bool conv_thread = tid < 3 * kGdnDk;
   int ch = 0;
   if (tid < kGdnDk) ch = kh * kGdnDk + tid;
   else if (tid < 2 * kGdnDk) ch = kGdnHk * kGdnDk + kh * kGdnDk + (tid - kGdnDk);
-  else ch = 2 * kGdnHk * kGdnDk + h * kGdnDv + (tid - 2 * kGdnDk);
-  float w[kGdnConvK] = {0.f, 0.f, 0.f, 0.f}, hist[3] = {0.f, 0.f, 0.f};
-  if (conv_thread) {
-#pragma unroll
-    for (int i = 0; i < kGdnConvK; ++i) w[i] = bf2f(conv_w[ch * kGdnConvK + i]);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) hist[j] = bf2f(conv_in[ch * 3 + j]);
-  }
+  else if (conv_thread) ch = 2 * kGdnHk * kGdnDk + h * kGdnDv + (tid - 2 * kGdnDk);
+  const bf16x4 w_raw = *reinterpret_cast<const bf16x4*>(conv_w + ch * kGdnConvK);
+  const bf16 h0_raw = conv_in[ch * 3], h1_raw = conv_in[ch * 3 + 1], h2_raw = conv_in[ch * 3 + 2];
+  // the first token's inputs: x channel, a and b of this head, z columns
+  bf16 x_raw = x[ch];
+  bf16 a_raw = a[h], b_raw = b[h];
+  bf16x4 z_raw = *reinterpret_cast<const bf16x4*>(z + h * kGdnDv + 4 * cq);
 
   // ---- state tile --------------------------------------------------------
   const size_t sbase = (size_t)h * kGdnDk * kGdnDv + 4 * cq;
@@ -81,24 +84,24 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
     s[i] = *reinterpret_cast<const f32x4*>(state_in + sbase + (size_t)(r0 + i) * kGdnDv);
   const float A = expf(a_log[h]);
   const float dtb = dt_bias[h];
-  float nw[4] = {0.f, 0.f, 0.f, 0.f};
-  if (rg == 0) {
+  const bf16x4 nw_raw = *reinterpret_cast<const bf16x4*>(norm_w + 4 * cq);
+  float w[kGdnConvK], hist[3], nw[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) nw[e] = bf2f(norm_w[4 * cq + e]);
-  }
+  for (int i = 0; i < kGdnConvK; ++i) w[i] = bf2f(w_raw[i]);
+  hist[0] = bf2f(h0_raw);
+  hist[1] = bf2f(h1_raw);
+  hist[2] = bf2f(h2_raw);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) nw[e] = bf2f(nw_raw[e]);
 
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
   for (unsigned t = 0; t < tokens; ++t) {
     const int par = t & 1;
-    // z of this token for the gated norm (wave 0, lanes 0..31), requested
-    // with the token's other inputs so its round trip is not paid after
-    // the delta rule
-    bf16x4 zrow;
-    if (wave == 0 && lane < 32)
-      zrow = *reinterpret_cast<const bf16x4*>(z + (size_t)t * z_row_stride + h * kGdnDv + 4 * cq);
+    const float cur = bf2f(x_raw);
+    const float av = bf2f(a_raw), bv = bf2f(b_raw);
+    const bf16x4 zrow = z_raw;
     // -- phase A: conv + SiLU (bf16-rounded, as the conv kernel), gating --
     if (conv_thread) {
-      const float cur = bf2f(x[(size_t)t * x_row_stride + ch]);
       float acc = ds_mul(hist[0], w[0]);
       acc = ds_add(acc, ds_mul(hist[1], w[1]));
       acc = ds_add(acc, ds_mul(hist[2], w[2]));
@@ -109,14 +112,21 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
       hist[1] = hist[2];
       hist[2] = cur;
     } else if (tid == 3 * kGdnDk) {
-      const float av = bf2f(a[(size_t)t * ab_row_stride + h]);
-      const float bv = bf2f(b[(size_t)t * ab_row_stride + h]);
       const float xs = ds_add(av, dtb);
       const float sp = xs > 20.0f ? xs : log1pf(expf(xs));
       gb[par][0] = ds_mul(-A, sp);
       gb[par][1] = bf2f(f2bf(1.0f / (1.0f + expf(-bv))));   // sigmoid of bf16 b, in bf16
     }
     __syncthreads();
+    // request the next token's inputs (this token's are consumed; the last
+    // token re-reads its own row, so every load stays in bounds)
+    {
+      const size_t tn = t + 1 < tokens ? t + 1 : t;
+      x_raw = x[tn * x_row_stride + ch];
+      a_raw = a[tn * ab_row_stride + h];
+      b_raw = b[tn * ab_row_stride + h];
+      z_raw = *reinterpret_cast<const bf16x4*>(z + tn * z_row_stride + h * kGdnDv + 4 * cq);
+    }
     const float* qv = ych[par];
     const float* kvec = ych[par] + kGdnDk;
     const float* vvec = ych[par] + 2 * kGdnDk;
@@ -169,7 +179,6 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
     }
 #pragma unroll
     for (int i = 0; i < kDsRowsPerThread; ++i) s[i] = s[i] * eg + delta * (kvec[r0 + i] * kinv);
-
     // -- phase C: gated RMSNorm over the head's 128 outputs (wave 0, lanes
     // 0..31 hold 4 columns each; every row group holds the same o) --
     if (wave == 0) {
@@ -198,7 +207,6 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
 #pragma unroll
   for (int i = 0; i < kDsRowsPerThread; ++i)
     *reinterpret_cast<f32x4*>(state_out + sbase + (size_t)(r0 + i) * kGdnDv) = s[i];
-  // new conv state: v channels by their head, q/k channels by the even head
   if (conv_thread && (tid >= 2 * kGdnDk || (h & 1) == 0)) {
 #pragma unroll
     for (int j = 0; j < 3; ++j) conv_out[ch * 3 + j] = f2bf(hist[j]);

@@ -44,7 +44,7 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
     p.add_argument("--only", choices=["decode", "prefill", "prefill_8k", "prefill_c3", "gdn", "moe",
-                                      "moe_decode", "gemm", "copy"], default=None,
+                                      "moe_decode", "gemm", "copy", "launch"], default=None,
                    help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
 
@@ -770,6 +770,34 @@ def cpu_gdn_baseline(torch, chunk_tokens=512, steps=8):
                       f"{_cpu_info()})"}
 
 
+def bench_launch_cost(torch, dev, launches=30, iters=50, warmup=5):
+    """The fixed cost of one kernel node in a HIP graph: ``launches``
+    back-to-back launches of a one-element kernel (torch's fill, and this
+    library's output gate over one row), replayed as one graph; reported
+    per launch.  Every per-layer latency in a decode step pays this once
+    per kernel."""
+    from qwen36_attn import _lib
+    x = torch.zeros(1, device=dev)
+    attn = torch.zeros(1, 4096, dtype=torch.bfloat16, device=dev)
+    qg = torch.zeros(1, 8192, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(1, 4096, dtype=torch.bfloat16, device=dev)
+
+    def fills():
+        for _ in range(launches):
+            x.zero_()
+
+    def gates():
+        st = torch.cuda.current_stream().cuda_stream
+        for _ in range(launches):
+            _lib.call("qwen36_output_gate", attn.data_ptr(), 0, qg.data_ptr(), 8192,
+                      out.data_ptr(), 1, st)
+    tm = Timer(torch)
+    res = {"launches": launches}
+    for name, fn in (("torch_fill", fills), ("output_gate_1row", gates)):
+        res[name + "_us_per_launch"] = tm.time(make_graph(torch, fn).replay, iters, warmup) * 1e3 / launches
+    return res
+
+
 def run_only(torch, fa, dev, args):
     """Single legs for counter runs (rocprofv3 --pmc): the decode headline
     (10 layers x S=131072, eager launches), the prefill configs, the GDN legs,
@@ -792,6 +820,8 @@ def run_only(torch, fa, dev, args):
              bench_gdn_fused_gating_update(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_decode_step(torch, dev, GDN_LAYERS, args.steps, args.warmup, False),
              bench_gdn_prefill(torch, dev, 8192, args.steps, args.warmup)]
+    elif args.only == "launch":
+        r = bench_launch_cost(torch, dev)
     elif args.only == "moe":
         r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup)]
     elif args.only == "moe_decode":
@@ -836,6 +866,7 @@ def main():
                                                                  fused=False),
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
+        "graph_launch_cost": bench_launch_cost(torch, dev),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "gdn_fused_gating_update_30layers": bench_gdn_fused_gating_update(torch, dev, GDN_LAYERS,
                                                                           50, 5, use_graph),
