@@ -62,6 +62,9 @@ SIGNATURES: dict[str, tuple] = {
                                                      _vp, _u32, _u32, _f32, _u32, _vp]),
     "qwen36_gdn_gated_norm": (_i32, [_vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     # prefill projections
+    "qwen36_prefill_gemm_lt_workspace_bytes": (_sz, []),
+    "qwen36_prefill_gemm_bf16_lt": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _sz,
+                                           _vp]),
     "qwen36_prefill_gemm_bf16": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "qwen36_prefill_gemm_workspace_bytes": (_sz, [_u32, _u32, _u32]),
     "qwen36_prefill_gemm_bf16_ws": (_i32, [_vp, _u32, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _sz,

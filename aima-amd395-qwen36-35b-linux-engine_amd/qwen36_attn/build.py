@@ -73,7 +73,8 @@ def build_library(verbose: bool = False) -> str:
                         print(err, file=sys.stderr)
         tmp_lib = LIB_PATH + ".tmp"
         _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC",
-              *[o for _, o in jobs], "-o", tmp_lib])
+              *[o for _, o in jobs], "-o", tmp_lib, "-L", os.path.join(ROCM, "lib"),
+              "-lhipblaslt", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}"])
     os.replace(tmp_lib, LIB_PATH)
     build_harness(verbose)
     return LIB_PATH

@@ -302,11 +302,13 @@ def bench_decode_projections(torch, dev, iters, warmup, use_graph, native=True, 
 PREFILL_PROJ_SHAPES = [(9216, 2048), (2048, 4096), (12352, 2048), (2048, 4096)]
 
 
-def bench_prefill_projections(torch, dev, t, iters, warmup, native=True, seed=13):
+def bench_prefill_projections(torch, dev, t, iters, warmup, native=True, seed=13,
+                              backend="auto"):
     """The prefill projections of one full-attention layer (fused q|gate,k,v
     [9216, 2048] and o_proj [2048, 4096]) and one Gated-DeltaNet layer
     (fused qkv|z|b|a [12352, 2048] and out_proj [2048, 4096]) for a prompt
-    of t tokens: the HIP MFMA GEMM (``native``) or torch.matmul (hipBLASLt)."""
+    of t tokens: the library's ``linear`` (``native``; ``backend`` "auto" =
+    its hipBLASLt entry point, "native" = its MFMA kernel) or torch.matmul."""
     from qwen36_attn.prefill_gemm import linear
     gen = torch.Generator(device=dev).manual_seed(seed)
     ws = [(torch.randn(n, k, generator=gen, device=dev) * 0.02).to(torch.bfloat16)
@@ -319,7 +321,7 @@ def bench_prefill_projections(torch, dev, t, iters, warmup, native=True, seed=13
         for w, o in zip(ws, outs):
             x = xs[w.shape[1]]
             if native:
-                linear(x, w, out=o)
+                linear(x, w, out=o, backend=backend)
             else:
                 torch.matmul(x, w.t(), out=o)
     ms = Timer(torch).time(step, iters, warmup)
@@ -887,6 +889,10 @@ def main():
         "prefill_projections_8k": bench_prefill_projections(torch, dev, 8192, 10, 2),
         "prefill_projections_8k_torch": bench_prefill_projections(torch, dev, 8192, 10, 2,
                                                                   native=False),
+        "prefill_projections_8k_mfma_kernel": bench_prefill_projections(torch, dev, 8192, 10, 2,
+                                                                        backend="native"),
+        "prefill_projections_1k_mfma_kernel": bench_prefill_projections(torch, dev, 1024, 20, 3,
+                                                                        backend="native"),
         "moe_prefill_8k": bench_moe_prefill(torch, dev, 8192, 10, 2),
         "moe_prefill_1k": bench_moe_prefill(torch, dev, 1024, 20, 3),
         "moe_prefill_8k_torch_expert_loop": bench_moe_prefill(torch, dev, 8192, 3, 1, native=False),

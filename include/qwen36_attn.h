@@ -316,6 +316,21 @@ int qwen36_prefill_gemm_bf16(const void* x, unsigned ldx, const void* w, void* y
  * many bytes, else the call returns the invalid-argument code.  Same
  * reference call sites as qwen36_prefill_gemm_bf16. */
 size_t qwen36_prefill_gemm_workspace_bytes(unsigned m, unsigned n, unsigned k);
+/* qwen36_prefill_gemm_bf16_lt: the same product (y = x W^T, bf16, fp32
+ * accumulation, one rounding) run as a hipBLASLt GEMM -- the library the
+ * reference's native prefill plans these projections with
+ * (native_full_prefill.hip.cpp:552-560) -- for the shapes where its kernel
+ * is faster than the MFMA kernel above.  Same arguments and limits as
+ * qwen36_prefill_gemm_bf16_ws, except that the workspace (caller-owned,
+ * qwen36_prefill_gemm_lt_workspace_bytes() bytes suffice for every shape)
+ * is what hipBLASLt's algorithm needs.  The first call of a shape on a device
+ * creates the library handle and queries the algorithm (host work only;
+ * make it outside graph capture).  Returns hipErrorNotSupported when
+ * hipBLASLt has no algorithm for the shape. */
+size_t qwen36_prefill_gemm_lt_workspace_bytes(void);
+int qwen36_prefill_gemm_bf16_lt(const void* x, unsigned ldx, const void* w, void* y,
+                                unsigned ldy, unsigned m, unsigned n, unsigned k, void* ws,
+                                size_t ws_bytes, void* stream);
 int qwen36_prefill_gemm_bf16_ws(const void* x, unsigned ldx, const void* w, void* y,
                                 unsigned ldy, unsigned m, unsigned n, unsigned k,
                                 void* ws, size_t ws_bytes, void* stream);

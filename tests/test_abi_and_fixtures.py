@@ -150,6 +150,13 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert G(1024, 2048, 4096) == 2 * 1024 * 2048 * 4
     assert G(256, 2048, 4096) % (256 * 2048 * 4) == 0 and G(256, 2048, 4096) > 0
     assert G(1024, 2048, 4000) == 0 and G(0, 2048, 4096) == 0
+    # hipBLASLt form: nulls, m = 0, ldy < n, workspace size without a buffer
+    lt = L.qwen36_prefill_gemm_bf16_lt
+    assert L.qwen36_prefill_gemm_lt_workspace_bytes() > 0
+    assert lt(None, 2048, 16, 16, 2048, 16, 2048, 2048, None, 0, None) == 1
+    assert lt(16, 2048, 16, 16, 2048, 0, 2048, 2048, None, 0, None) == 1
+    assert lt(16, 2048, 16, 16, 100, 16, 2048, 2048, None, 0, None) == 1
+    assert lt(16, 2048, 16, 16, 2048, 16, 2048, 2048, None, 64, None) == 1
     # shapes the launch rejects size no workspace
     assert G(1024, 2048, 16384 + 64) == 0 and G(1024, 65537, 4096) == 0
     assert G(262145, 2048, 4096) == 0
