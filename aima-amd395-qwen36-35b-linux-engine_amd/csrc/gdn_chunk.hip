@@ -292,32 +292,42 @@ __global__ __launch_bounds__(256, 2) void gdn_chunk_prep_kernel(
     const bool is_q = job >= 10;
     const int t = is_q ? job - 10 : job;
     const int rt = tri_row(t), ct = tri_col(t);
+    // Branch-free: every LDS scalar the four elements use is read first (one
+    // vector read per row of scalars), the decays of entries past the
+    // diagonal are computed and discarded by the selects (a select, not a
+    // product, so an infinite exp2 there cannot leak).
     if (is_q) {
       // lane holds Aqk[i][j] for i = 16rt + li, j = 16ct + 4lg + r: exactly
       // half of its A-operand fragment (column block ct/2, half ct%2)
-      const int i = 16 * rt + li;
+      const int i = 16 * rt + li, j0 = 16 * ct + 4 * lg;
+      const float gi = s.gs[i], qsi = s.qinv[i] * kQScale;
+      const f32x4 gj = *reinterpret_cast<const f32x4*>(s.gs + j0);
+      const f32x4 kj = *reinterpret_cast<const f32x4*>(s.kinv + j0);
       bf16x4 vh, vl;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int j = 16 * ct + 4 * lg + r;
-        const float decay = j <= i ? __builtin_amdgcn_exp2f((s.gs[i] - s.gs[j]) * kLog2e) : 0.f;
-        const float a = j <= i ? (((s.qinv[i] * kQScale) * s.kinv[j]) * acc_job[jj][r]) * decay : 0.f;
+        const bool on = j0 + r <= i;
+        const float decay = __builtin_amdgcn_exp2f((gi - gj[r]) * kLog2e);
+        const float a = on ? ((qsi * kj[r]) * acc_job[jj][r]) * decay : 0.f;
         bf16 hh, ll;
         split2(a, hh, ll);
         vh[r] = hh;
         vl[r] = ll;
       }
-      const int o = frag_off(i, 16 * ct + 4 * lg, 2);
+      const int o = frag_off(i, j0, 2);
       *reinterpret_cast<bf16x4*>(ah + o) = vh;
       *reinterpret_cast<bf16x4*>(al + o) = vl;
     } else {
-      const int j = 16 * ct + li;
+      const int j = 16 * ct + li, i0 = 16 * rt + 4 * lg;
+      const float gj = s.gs[j], kj = s.kinv[j];
+      const f32x4 gi = *reinterpret_cast<const f32x4*>(s.gs + i0);
+      const f32x4 ki = *reinterpret_cast<const f32x4*>(s.kinv + i0);
+      const f32x4 bi = *reinterpret_cast<const f32x4*>(s.bs + i0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int i = 16 * rt + 4 * lg + r;
-        const float decay = j <= i ? __builtin_amdgcn_exp2f((s.gs[i] - s.gs[j]) * kLog2e) : 0.f;
-        s.u.lm[i * kPitchF + j] =
-            j < i ? (((s.kinv[i] * s.kinv[j]) * acc_job[jj][r]) * s.bs[i]) * decay : 0.f;
+        const float decay = __builtin_amdgcn_exp2f((gi[r] - gj) * kLog2e);
+        s.u.lm[(i0 + r) * kPitchF + j] =
+            j < i0 + r ? (((ki[r] * kj) * acc_job[jj][r]) * bi[r]) * decay : 0.f;
       }
     }
   }
