@@ -540,7 +540,112 @@ Q36_EXPORT int qrt_ck_fmha_bf16_launch_ex(const void* q, const void* k,
 Q36_EXPORT int qrt_ck_fmha_release(void) { return Q36_OK; }
 
 // Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300).
-Q36_EXPORT int qrt_ck_fmha_q8192_prepare(void) { return Q36_OK; }
+// The fp32-packed launch takes rows of [q (4096) | 4096 more q_proj features
+// | k (512) | v (512)] fp32 (9216 per token, the q_proj + k_proj + v_proj
+// outputs side by side), rounds q, k and v to bf16 into provider staging
+// (q8192_prepare allocates it, 80 MiB per device; q8192_release frees it),
+// and runs the square causal attention over the staged tensors.
+namespace q36 {
+namespace {
+constexpr unsigned kQ8192 = 8192u;
+constexpr unsigned kPackedRow = 2u * kQDim + 2u * kKvRow;   // 9216
+
+// thread = 8 consecutive features of one token's q, k or v
+__global__ __launch_bounds__(256) void fmha_pack_q8192_kernel(const float* __restrict__ packed,
+                                                             bf16* __restrict__ qs,
+                                                             bf16* __restrict__ ks,
+                                                             bf16* __restrict__ vs) {
+  constexpr unsigned kPerTok = (kQDim + 2u * kKvRow) / 8u;   // 640 octets per token
+  const unsigned idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= kQ8192 * kPerTok) return;
+  const unsigned tok = idx / kPerTok, o = idx % kPerTok;
+  const float* src;
+  bf16* dst;
+  if (o < kQDim / 8u) {
+    src = packed + (size_t)tok * kPackedRow + 8u * o;
+    dst = qs + (size_t)tok * kQDim + 8u * o;
+  } else if (o < (kQDim + kKvRow) / 8u) {
+    const unsigned f = 8u * o - kQDim;
+    src = packed + (size_t)tok * kPackedRow + 2u * kQDim + f;
+    dst = ks + (size_t)tok * kKvRow + f;
+  } else {
+    const unsigned f = 8u * o - kQDim - kKvRow;
+    src = packed + (size_t)tok * kPackedRow + 2u * kQDim + kKvRow + f;
+    dst = vs + (size_t)tok * kKvRow + f;
+  }
+  const f32x4 a = reinterpret_cast<const f32x4*>(src)[0];
+  const f32x4 b = reinterpret_cast<const f32x4*>(src)[1];
+  // round to nearest even (NaN stays NaN), as the provider's packing does
+  *reinterpret_cast<bf16x8*>(dst) = bf16x8{f2bf(a[0]), f2bf(a[1]), f2bf(a[2]), f2bf(a[3]),
+                                           f2bf(b[0]), f2bf(b[1]), f2bf(b[2]), f2bf(b[3])};
+}
+
+struct Q8192Staging {
+  bf16* q = nullptr;
+  bf16* k = nullptr;
+  bf16* v = nullptr;
+};
+Q8192Staging g_q8192[kFmMaxDevices];
+
+// Allocates the current device's staging if absent (caller holds g_fm_mutex).
+int q8192_prepare_locked(int dev) {
+  Q8192Staging& st = g_q8192[dev];
+  if (st.q != nullptr) return Q36_OK;
+  const size_t qb = (size_t)kQ8192 * kQDim * 2, kvb = (size_t)kQ8192 * kKvRow * 2;
+  void *q = nullptr, *k = nullptr, *v = nullptr;
+  hipError_t e = hipMalloc(&q, qb);
+  if (e == hipSuccess) e = hipMalloc(&k, kvb);
+  if (e == hipSuccess) e = hipMalloc(&v, kvb);
+  if (e != hipSuccess) {
+    (void)hipFree(q);
+    (void)hipFree(k);
+    (void)hipFree(v);
+    return static_cast<int>(e);
+  }
+  st.q = static_cast<bf16*>(q);
+  st.k = static_cast<bf16*>(k);
+  st.v = static_cast<bf16*>(v);
+  return Q36_OK;
+}
+
+int current_device(int* dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= kFmMaxDevices) {
+    (void)hipGetLastError();
+    return static_cast<int>(hipErrorInvalidDevice);
+  }
+  return Q36_OK;
+}
+}  // namespace
+}  // namespace q36
+
+Q36_EXPORT int qrt_ck_fmha_q8192_prepare(void) {
+  int dev = 0;
+  const int e = q36::current_device(&dev);
+  if (e != Q36_OK) return e;
+  std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
+  return q36::q8192_prepare_locked(dev);
+}
+
+Q36_EXPORT int qrt_ck_fmha_q8192_f32_launch(const float* packed_qkv, float* out, void* stream) {
+  if (packed_qkv == nullptr || out == nullptr) return Q36_EINVAL;
+  int dev = 0;
+  int e = q36::current_device(&dev);
+  if (e != Q36_OK) return e;
+  q36::Q8192Staging st;
+  {
+    std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
+    e = q36::q8192_prepare_locked(dev);
+    if (e != Q36_OK) return e;
+    st = q36::g_q8192[dev];
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  constexpr unsigned kThreads = q36::kQ8192 * ((q36::kQDim + 2u * q36::kKvRow) / 8u);
+  hipLaunchKernelGGL(q36::fmha_pack_q8192_kernel, dim3((kThreads + 255u) / 256u), dim3(256), 0,
+                     s, packed_qkv, st.q, st.k, st.v);
+  const hipError_t le = hipGetLastError();
+  if (le != hipSuccess) return static_cast<int>(le);
+  return q36::provider_launch(st.q, st.k, st.v, out, q36::kQ8192, q36::kQ8192, s);
+}
 
 Q36_EXPORT int qrt_ck_fmha_q8192_bf16_launch(const void* q, const void* k,
                                              const void* v, float* out,
@@ -549,7 +654,19 @@ Q36_EXPORT int qrt_ck_fmha_q8192_bf16_launch(const void* q, const void* k,
                               static_cast<hipStream_t>(stream));
 }
 
-Q36_EXPORT int qrt_ck_fmha_q8192_release(void) { return Q36_OK; }
+// Frees the fp32 path's staging (the caller has finished every launch that
+// uses it, as with the reference's release).
+Q36_EXPORT int qrt_ck_fmha_q8192_release(void) {
+  int dev = 0;
+  if (q36::current_device(&dev) != Q36_OK) return Q36_OK;
+  std::lock_guard<std::mutex> lock(q36::g_fm_mutex);
+  q36::Q8192Staging& st = q36::g_q8192[dev];
+  (void)hipFree(st.q);
+  (void)hipFree(st.k);
+  (void)hipFree(st.v);
+  st = q36::Q8192Staging{};
+  return Q36_OK;
+}
 
 // ---- workspace form (no counterpart in the reference's provider ABI) -------
 Q36_EXPORT size_t qwen36_fmha_prefill_workspace_bytes(unsigned query_tokens,

@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple] = {
     "qwen36_fmha_prefill": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _sz, _vp]),
     "qrt_ck_fmha_q8192_prepare": (_i32, []),
     "qrt_ck_fmha_q8192_bf16_launch": (_i32, [_vp, _vp, _vp, _vp, _vp]),
+    "qrt_ck_fmha_q8192_f32_launch": (_i32, [_vp, _vp, _vp]),
     "qrt_ck_fmha_q8192_release": (_i32, []),
     # decode
     "qwen36_decode_gqa_workspace_bytes": (_sz, [_u32, _u32]),

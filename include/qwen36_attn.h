@@ -63,9 +63,15 @@ size_t qwen36_fmha_prefill_workspace_bytes(unsigned query_tokens, unsigned kv_to
 int qwen36_fmha_prefill(const void* q, const void* k, const void* v, float* out,
                         unsigned query_tokens, unsigned kv_tokens, void* workspace,
                         size_t workspace_bytes, void* stream);
-/* Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300);
- * the fp32-packed q8192 launch is not provided. */
+/* Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300).
+ * qrt_ck_fmha_q8192_f32_launch (:228-271): packed_qkv fp32 [8192, 9216] rows
+ * of [q (4096) | 4096 more q_proj features, unused | k (512) | v (512)],
+ * rounded to bf16 (nearest even) into provider staging -- 80 MiB per device,
+ * allocated by q8192_prepare or the first f32 launch, freed by
+ * q8192_release -- then the square causal attention into out fp32
+ * [8192, 4096]. */
 int qrt_ck_fmha_q8192_prepare(void);
+int qrt_ck_fmha_q8192_f32_launch(const float* packed_qkv, float* out, void* stream);
 int qrt_ck_fmha_q8192_bf16_launch(const void* q, const void* k, const void* v,
                                   float* out, void* stream);
 int qrt_ck_fmha_q8192_release(void);

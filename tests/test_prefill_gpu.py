@@ -279,3 +279,30 @@ def test_split_prefill_ignores_stale_workspace(gpu):
     b = fmha_prefill(qd, kd, vd)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_q8192_f32_packed_launch(gpu):
+    """The legacy fp32-packed provider launch (qrt_ck_fmha_q8192_f32_launch,
+    qrt_ck_fmha_q8192_provider.cpp:228-271): rows [q | unused | k | v] of
+    9216 fp32 values, rounded to bf16 and attended causally over 8192
+    tokens -- equal, bit for bit, to the bf16 launch on the same rounded
+    tensors; a second call after release re-allocates the staging."""
+    from qwen36_attn import _lib
+    from qwen36_attn.full_attention import fmha_prefill
+    lib = _lib.load()
+    g = torch.Generator(device=gpu).manual_seed(8192)
+    packed = torch.randn(8192, 9216, generator=g, device=gpu)
+    q = packed[:, :4096].to(torch.bfloat16).view(8192, 16, 256).contiguous()
+    k = packed[:, 8192:8704].to(torch.bfloat16).view(8192, 2, 256).contiguous()
+    v = packed[:, 8704:].to(torch.bfloat16).view(8192, 2, 256).contiguous()
+    print("q8192 f32 packed launch", flush=True)
+    ref = fmha_prefill(q, k, v)
+    h = torch.cuda.current_stream(gpu).cuda_stream
+    for _ in range(2):
+        out = torch.full((8192, 4096), float("nan"), device=gpu)
+        assert lib.qrt_ck_fmha_q8192_prepare() == 0
+        assert lib.qrt_ck_fmha_q8192_f32_launch(packed.data_ptr(), out.data_ptr(), h) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        assert lib.qrt_ck_fmha_q8192_release() == 0
+    assert lib.qrt_ck_fmha_q8192_f32_launch(None, out.data_ptr(), h) == 1
