@@ -394,14 +394,18 @@ def fused_sigmoid_gating_delta_rule_update(A_log, a, b, dt_bias, q, k, v, beta: 
     if initial_state.dim() != 4 or tuple(initial_state.shape[1:]) != (HV, DV, DK):
         raise ValueError("initial_state must be [slots, 32, 128, 128]")
     slots = initial_state.shape[0]
-    final = initial_state if inplace_final_state else initial_state.clone()
+    single = cu_seqlens is None and ssm_state_indices is None
+    # out of place: a single sequence writes every element of the new state;
+    # a batch leaves slots no sequence uses untouched, so it starts from a copy
+    final = (initial_state if inplace_final_state else
+             torch.empty_like(initial_state) if single else initial_state.clone())
     out = torch.empty(1, t, HV, DV, dtype=torch.bfloat16, device=qv.device)
     a_log = A_log.float().contiguous()
     dtb = dt_bias.float().contiguous()
     if scale is None:
         scale = DK ** -0.5
     flags = 1 if use_qk_l2norm_in_kernel else 0
-    if cu_seqlens is None and ssm_state_indices is None:
+    if single:
         if slots != 1:
             raise ValueError("a single sequence takes a [1, 32, 128, 128] state")
         _lib.call("qwen36_gdn_fused_gating_update", ptr(a_log), ptr(a2), ptr(b2), a2.stride(0),
