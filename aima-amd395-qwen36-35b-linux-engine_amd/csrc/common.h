@@ -55,6 +55,56 @@ constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 __device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }  // RNE
 
+// Sigmoid output gate of one attention value (native_pointwise.hip.cpp:
+// 207-222, :339-359): the attention rounded to bf16, sigmoid(gate) rounded
+// to bf16, their product rounded to bf16.  Shared by every kernel that
+// applies the gate so they round identically.
+__device__ __forceinline__ bf16 gate_bf16(float attn, bf16 gate) {
+  const bf16 a = f2bf(attn);
+  const bf16 sg = f2bf(1.0f / (1.0f + expf(-bf2f(gate))));
+  return f2bf(__fmul_rn(bf2f(a), bf2f(sg)));
+}
+
+// gate_bf16 for four values, with the sigmoid from the hardware exp2 and
+// reciprocal.  g is bf16 (8 significant bits) and log2(e)'s high part has
+// 16, so g * kLog2eHi is exact and the low part enters as a first-order
+// factor: e^-g = 2^(-g kLog2eHi) (1 - g kLn2Lo) within ~2 ulps, 1/(1 + e^-g)
+// within ~4, the exact form's expf and division within 2 -- so unless the
+// fast value lies within 32 ulps of a bf16 rounding midpoint (low 16 bits
+// 0x8000) both round to the same bf16.  Such values (about 1 in 1000), |g|
+// > 60 and non-finite g take the exact form; the group of four branches
+// once.  Same bits as gate_bf16 for every non-NaN gate (checked over all
+// 65536 bf16 gates; a NaN gate gives a NaN) at a fraction of the
+// instructions -- for epilogues, where the gate's math is not spread over a
+// whole elementwise launch.
+constexpr float kLog2eHi = 1.44268798828125f;       // 47274 / 2^15
+constexpr float kLn2Lo = 4.888495152129525e-06f;    // (log2(e) - kLog2eHi) ln 2
+__device__ __forceinline__ bf16x4 gate4_bf16_fast(const f32x4& attn, const bf16x4& gate) {
+  float sg[4];
+  bool slow = false;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float g = bf2f(gate[e]);
+    const float th = __builtin_amdgcn_exp2f(g * -kLog2eHi);
+    const float t = __builtin_fmaf(th, g * -kLn2Lo, th);
+    sg[e] = __builtin_amdgcn_rcpf(1.0f + t);
+    const int mid = (int)(__float_as_uint(sg[e]) & 0xffffu) - 0x8000;
+    slow |= !(fabsf(g) <= 60.0f) || (mid >= -32 && mid <= 32);
+  }
+  if (slow) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g = bf2f(gate[e]);
+      const int mid = (int)(__float_as_uint(sg[e]) & 0xffffu) - 0x8000;
+      if (!(fabsf(g) <= 60.0f) || (mid >= -32 && mid <= 32)) sg[e] = 1.0f / (1.0f + expf(-g));
+    }
+  }
+  bf16x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = f2bf(__fmul_rn(bf2f(f2bf(attn[e])), bf2f(f2bf(sg[e]))));
+  return o;
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }

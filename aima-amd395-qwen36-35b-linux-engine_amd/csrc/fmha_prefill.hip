@@ -59,6 +59,10 @@ constexpr int kKTile = 16 * kKBlk;                    // 16640
 constexpr int kVTile = 16 * kVBlk;                    // 17408
 constexpr int kFmStage = kKTile + kVTile;             // 34048
 constexpr int kFmLds = 2 * kFmStage;                  // 68096: double buffer
+// Gated kernels also prefetch the gate values of output rounds 0-1 (dims
+// 0-127 of the head) of their 256 rows into LDS after the ring.
+constexpr int kFmGateLds = 256 * 256;
+constexpr int kFmLdsGated = kFmLds + kFmGateLds;      // 133632
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -71,11 +75,21 @@ struct SplitArgs {
   unsigned n_chunks;
 };
 
-template <int kFmWaves, bool kSplit>
+// Gated output (kGate): out_bf16[row][h*256 + d] = gate_bf16(O, gate[row *
+// gate_stride + h*512 + 256 + d]) -- the gate half of each head's 512-wide
+// slice of the fused q projection -- in place of the fp32 attention rows.
+struct GateArgs {
+  const bf16* gate;
+  unsigned gate_stride;   // elements between token rows of the q projection
+  bf16* out;
+};
+
+template <int kFmWaves, bool kSplit, bool kGate = false>
 __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k,
     const bf16* __restrict__ v, float* __restrict__ out, unsigned q_tokens,
-    unsigned kv_tokens, unsigned n_qtiles, SplitArgs sp) {
+    unsigned kv_tokens, unsigned n_qtiles, SplitArgs sp, GateArgs ga) {
+  static_assert(!(kSplit && kGate), "split partials are gated by the combine");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int kFmRows = kFmWaves * kFmRowsPerWave;
   constexpr int kFmLoadsPerWave = 16 / kFmWaves;       // 16 row-pair blocks per tile
@@ -140,6 +154,22 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
       __builtin_amdgcn_make_buffer_rsrc((void*)v, 0, nrec, 0x00020000);
   const int fvoff = (kFmLoadsPerWave * wave + 16 * (lane >> 5)) * kTokBytes +
                     kvh * kRowBytes + (lane & 31) * 16;
+  // gated: the gate values of output rounds 0-1 of this workgroup's rows
+  // (row-major [256 rows][256 B]), fetched now so they are resident when the
+  // epilogue starts; rows past the end read as zeros.
+  if constexpr (kGate) {
+    const unsigned rows_here = min(q_tokens - q0, (unsigned)kFmRows);
+    const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(ga.gate) + (size_t)q0 * ga.gate_stride + head * 2 * kD + kD, 0,
+        (int)(rows_here * ga.gate_stride * 2), 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r0 = wave * kFmRowsPerWave + 4 * j;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          grs, (lds_void*)(lds + kFmLds + r0 * 256), 16,
+          (int)(((r0 + (lane >> 4)) * ga.gate_stride) * 2 + (lane & 15) * 16), 0, 0, 0);
+    }
+  }
   auto fetch = [&](unsigned kv0, int stage) {
     char* ks = lds + stage * kFmStage;
     char* vs = ks + kKTile;
@@ -296,9 +326,25 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
     // and stores whole 256-byte row segments, instead of 32-byte pieces of
     // 32 rows per store instruction.
     const float inv = row_valid ? 1.0f / l : 0.f;
+    const unsigned wrow0 = q0 + wave * kFmRowsPerWave;
+    // gated: rounds 0-1 take their gate values from the LDS prefetch; the
+    // register loads of rounds 2-3 are issued now and land behind rounds 0-1
+    // (rows past the end read the last row's and are not stored)
+    bf16x4 gv[2][8];
+    if constexpr (kGate) {
+      __builtin_amdgcn_s_waitcnt(0);   // this wave's gate prefetch landed
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd)
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const unsigned r = min(wrow0 + it * 4 + (lane >> 4), q_tokens - 1);
+          gv[rd][it] = *reinterpret_cast<const bf16x4*>(
+              ga.gate + (size_t)r * ga.gate_stride + head * 2 * kD + kD + (rd + 2) * 64 +
+              (lane & 15) * 4);
+        }
+    }
     __syncthreads();   // every wave is done with the K/V ring
     char* stg = lds + wave * 8192;
-    const unsigned wrow0 = q0 + wave * kFmRowsPerWave;
 #pragma unroll
     for (int rd = 0; rd < 4; ++rd) {
 #pragma unroll
@@ -319,11 +365,21 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
       for (int it = 0; it < 8; ++it) {
         const int r = it * 4 + (lane >> 4), ch = lane & 15;
         const f32x4 v = *reinterpret_cast<const f32x4*>(stg + r * 256 + ((ch ^ (r & 15)) * 16));
-        if (wrow0 + r < q_tokens)
+        if constexpr (kGate) {
+          if (wrow0 + r < q_tokens) {
+            const bf16x4 g4 =
+                rd < 2 ? *reinterpret_cast<const bf16x4*>(lds + kFmLds + (wave * kFmRowsPerWave + r) * 256 +
+                                                          rd * 128 + ch * 8)
+                       : gv[rd - 2][it];
+            *reinterpret_cast<bf16x4*>(ga.out + (size_t)(wrow0 + r) * kQDim + head * kD +
+                                       rd * 64 + ch * 4) = gate4_bf16_fast(v, g4);
+          }
+        } else if (wrow0 + r < q_tokens) {
           // nontemporal: the output is not re-read here (459.0 vs 460.0 us at 8K)
           __builtin_nontemporal_store(
               v, reinterpret_cast<f32x4*>(out + (size_t)(wrow0 + r) * kQDim + head * kD +
                                           rd * 64 + ch * 4));
+        }
       }
       __atomic_signal_fence(__ATOMIC_SEQ_CST);
     }
@@ -336,7 +392,8 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
 // grid = tiles x 16 heads x 16 row groups; block = 512 (16 rows x 32 dims/8).
 __global__ __launch_bounds__(512) void fmha_split_combine_kernel(
     const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
-    unsigned q_tokens, unsigned kv_tokens, unsigned chunk_keys, unsigned n_chunks) {
+    unsigned q_tokens, unsigned kv_tokens, unsigned chunk_keys, unsigned n_chunks,
+    GateArgs ga) {
   constexpr int kRows = 256;
   const unsigned rg = blockIdx.x % 16, head = (blockIdx.x / 16) % kHq, qtile = blockIdx.x / (16 * kHq);
   const unsigned r = rg * 16 + (threadIdx.x >> 5);
@@ -368,6 +425,17 @@ __global__ __launch_bounds__(512) void fmha_split_combine_kernel(
     }
   }
   const float inv = 1.0f / L;
+  if (ga.out != nullptr) {   // gated bf16 rows (see GateArgs)
+    const bf16x8 g = *reinterpret_cast<const bf16x8*>(ga.gate + (size_t)row * ga.gate_stride +
+                                                      head * 2 * kD + kD + d0);
+    const bf16x4 lo = gate4_bf16_fast(f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv},
+                                      bf16x4{g[0], g[1], g[2], g[3]});
+    const bf16x4 hi = gate4_bf16_fast(f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv},
+                                      bf16x4{g[4], g[5], g[6], g[7]});
+    *reinterpret_cast<bf16x8*>(ga.out + (size_t)row * kQDim + head * kD + d0) =
+        bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return;
+  }
   f32x4* dst = reinterpret_cast<f32x4*>(out + (size_t)row * kQDim + head * kD + d0);
   dst[0] = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
   dst[1] = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
@@ -438,9 +506,11 @@ bool valid_geometry(const void* q, const void* k, const void* v, const float* ou
          q_tokens <= kMaxTokens && kv_tokens >= q_tokens && kv_tokens <= kMaxTokens;
 }
 
-// `scratch` null: run unsplit.
+// `scratch` null: run unsplit.  `ga.out` non-null: gated bf16 output (and
+// `out` unused).
 int launch_fmha(const void* q, const void* k, const void* v, float* out,
-                unsigned q_tokens, unsigned kv_tokens, void* scratch, hipStream_t stream) {
+                unsigned q_tokens, unsigned kv_tokens, void* scratch, hipStream_t stream,
+                const GateArgs& ga = GateArgs{nullptr, 0u, nullptr}) {
   std::call_once(g_fm_attr_once, [] {
     for (const void* f : {reinterpret_cast<const void*>(fmha_prefill_kernel<8, false>),
                           reinterpret_cast<const void*>(fmha_prefill_kernel<4, false>),
@@ -450,6 +520,10 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
           hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kFmLds);
       if (e != hipSuccess) g_fm_attr_status = e;
     }
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(fmha_prefill_kernel<8, false, true>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kFmLdsGated);
+    if (e != hipSuccess) g_fm_attr_status = e;
   });
   if (g_fm_attr_status != hipSuccess) return (int)g_fm_attr_status;
   auto tiles = [&](unsigned rows) { return (q_tokens + rows - 1) / rows; };
@@ -465,10 +539,15 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
     sp.chunk_keys = plan.chunk_keys;
     sp.n_chunks = plan.n_chunks;
     hipLaunchKernelGGL((fmha_prefill_kernel<8, true>), dim3(plan.items), dim3(512), kFmLds,
-                       stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), sp);
+                       stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), sp, ga);
     hipLaunchKernelGGL(fmha_split_combine_kernel, dim3(tiles(256) * kHq * 16), dim3(512), 0,
                        stream, sp.o, sp.ml, out, q_tokens, kv_tokens, plan.chunk_keys,
-                       plan.n_chunks);
+                       plan.n_chunks, ga);
+    return static_cast<int>(hipGetLastError());
+  }
+  if (ga.out != nullptr) {   // gated: 256-row workgroups at every length
+    hipLaunchKernelGGL((fmha_prefill_kernel<8, false, true>), dim3(tiles(256) * kHq), dim3(512),
+                       kFmLdsGated, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), none, ga);
     return static_cast<int>(hipGetLastError());
   }
   // Query rows per workgroup: 256 (8 waves) when that gives at least 256
@@ -478,13 +557,13 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
   // from T = 4096 and for 1024 rows over a 4096-token prefix).
   if (tiles(256) * kHq >= 256u || kv_tokens > q_tokens) {
     hipLaunchKernelGGL((fmha_prefill_kernel<8, false>), dim3(tiles(256) * kHq), dim3(512),
-                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), none);
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), none, ga);
   } else if (tiles(128) * kHq >= 256u) {
     hipLaunchKernelGGL((fmha_prefill_kernel<4, false>), dim3(tiles(128) * kHq), dim3(256),
-                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(128), none);
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(128), none, ga);
   } else {
     hipLaunchKernelGGL((fmha_prefill_kernel<2, false>), dim3(tiles(64) * kHq), dim3(128),
-                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(64), none);
+                       kFmLds, stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(64), none, ga);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -687,4 +766,22 @@ Q36_EXPORT int qwen36_fmha_prefill(const void* q, const void* k, const void* v, 
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return Q36_EINVAL;
   return q36::launch_fmha(q, k, v, out, query_tokens, kv_tokens, need > 0 ? workspace : nullptr,
                           static_cast<hipStream_t>(stream));
+}
+
+Q36_EXPORT int qwen36_fmha_prefill_gated(const void* q, const void* k, const void* v,
+                                         const void* q_gate, unsigned q_gate_row_stride,
+                                         void* out, unsigned query_tokens, unsigned kv_tokens,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  // (out stands in for the fp32 pointer in the geometry check)
+  if (!q36::valid_geometry(q, k, v, static_cast<const float*>(out), query_tokens, kv_tokens) ||
+      q_gate == nullptr || q_gate_row_stride < 2u * q36::kQDim ||
+      (reinterpret_cast<uintptr_t>(q_gate) & 7u) != 0 || (q_gate_row_stride & 7u) != 0 ||
+      (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+    return Q36_EINVAL;
+  const size_t need = q36::split_workspace_bytes(q36::split_plan(query_tokens, kv_tokens));
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return Q36_EINVAL;
+  const q36::GateArgs ga{static_cast<const q36::bf16*>(q_gate), q_gate_row_stride,
+                         static_cast<q36::bf16*>(out)};
+  return q36::launch_fmha(q, k, v, nullptr, query_tokens, kv_tokens,
+                          need > 0 ? workspace : nullptr, static_cast<hipStream_t>(stream), ga);
 }

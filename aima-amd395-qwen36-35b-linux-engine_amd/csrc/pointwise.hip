@@ -84,11 +84,9 @@ __global__ void output_gate_kernel(const void* __restrict__ attn,
   const size_t t = i / kQDim;
   const int f = (int)(i - t * kQDim);
   const int head = f / kD, d = f % kD;
-  const bf16 a = kF32 ? f2bf(static_cast<const float*>(attn)[i])
-                      : static_cast<const bf16*>(attn)[i];
-  const float gv = bf2f(q_gate[t * q_row_stride + head * 2 * kD + kD + d]);
-  const bf16 sg = f2bf(1.0f / (1.0f + expf(-gv)));
-  out[i] = f2bf(mul_rn(bf2f(a), bf2f(sg)));
+  const float a = kF32 ? static_cast<const float*>(attn)[i]
+                       : bf2f(static_cast<const bf16*>(attn)[i]);
+  out[i] = gate_bf16(a, q_gate[t * q_row_stride + head * 2 * kD + kD + d]);
 }
 
 std::mutex g_freq_mutex;   // first calls may come from several host threads

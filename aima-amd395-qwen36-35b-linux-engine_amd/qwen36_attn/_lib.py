@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple] = {
     "qrt_ck_fmha_release": (_i32, []),
     "qwen36_fmha_prefill_workspace_bytes": (_sz, [_u32, _u32]),
     "qwen36_fmha_prefill": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _vp, _sz, _vp]),
+    "qwen36_fmha_prefill_gated": (_i32, [_vp, _vp, _vp, _vp, _u32, _vp, _u32, _u32, _vp, _sz, _vp]),
     "qrt_ck_fmha_q8192_prepare": (_i32, []),
     "qrt_ck_fmha_q8192_bf16_launch": (_i32, [_vp, _vp, _vp, _vp, _vp]),
     "qrt_ck_fmha_q8192_f32_launch": (_i32, [_vp, _vp, _vp]),

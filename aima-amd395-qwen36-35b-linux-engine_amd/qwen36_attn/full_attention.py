@@ -154,6 +154,42 @@ def fmha_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     return out
 
 
+def fmha_prefill_gated(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       q_gate: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``fmha_prefill`` with the layer's sigmoid output gate applied in the
+    same launches: bf16 ``attn * sigmoid(gate)`` rows, bit-identical (for
+    non-NaN gates) to
+    ``output_gate(fmha_prefill(q, k, v), q_gate)`` (the reference runs the
+    provider FMHA and then full_attention_gate_kernel's f32 form,
+    native_full_prefill.hip.cpp:140-266, native_pointwise.hip.cpp:339-359).
+    q_gate: [T, 8192] bf16 with unit inner stride (e.g. the column view of
+    the fused q|gate|k|v projection).  Returns bf16 [T, 4096]."""
+    require(q, "q", torch.bfloat16)
+    require(k, "k", torch.bfloat16)
+    require(v, "v", torch.bfloat16)
+    t = q.shape[0]
+    s = k.shape[0]
+    if q.dim() != 3 or tuple(q.shape[1:]) != (HQ, HEAD_DIM):
+        raise ValueError("q must be [T, 16, 256]")
+    if k.dim() != 3 or tuple(k.shape[1:]) != (HKV, HEAD_DIM) or v.shape != k.shape:
+        raise ValueError("k/v must be [S, 2, 256]")
+    if not (0 < t <= MAX_TOKENS and t <= s <= MAX_TOKENS):
+        raise ValueError("FMHA geometry is invalid (need 0 < T <= S <= 262144)")
+    require(q_gate, "q_gate", torch.bfloat16, contiguous=False)
+    if q_gate.shape != (t, 2 * Q_DIM) or q_gate.stride(1) != 1:
+        raise ValueError("q_gate must be [T, 8192] with unit inner stride")
+    if out is None:
+        out = torch.empty(t, Q_DIM, dtype=torch.bfloat16, device=q.device)
+    require(out, "out", torch.bfloat16, shape=(t, Q_DIM))
+    lib = _lib.load(("qwen36_fmha_prefill_gated",))
+    nb = lib.qwen36_fmha_prefill_workspace_bytes(t, s)
+    ws = scratch("fmha_split", nb, q.device) if nb else None
+    _lib.call("qwen36_fmha_prefill_gated", ptr(q), ptr(k), ptr(v), ptr(q_gate), q_gate.stride(0),
+              ptr(out), t, s, ptr(ws), ws.numel() if ws is not None else 0,
+              stream_handle(q.device))
+    return out
+
+
 class FmhaProvider:
     """Python mirror of the reference's ctypes FMHA provider wrapper
     (``Q8192CompoundProvider.prepare`` / ``launch_ck_fmha``,
@@ -318,8 +354,8 @@ class FullAttentionLayer:
         else:
             q = head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"],
                                         self.k_cache, self.v_cache, position_start)
-            attn32 = fmha_prefill(q, self.k_cache[:cache_end], self.v_cache[:cache_end])
-            attn = output_gate(attn32, q_gate)
+            attn = fmha_prefill_gated(q, self.k_cache[:cache_end], self.v_cache[:cache_end],
+                                      q_gate)
         return linear(attn, w["o_proj"])
 
 

@@ -173,8 +173,7 @@ def full_attention(inp: torch.Tensor, layer_index: int, weights: dict) -> torch.
     q_gate, k, v = proj.split_rows(pg.linear(inp, proj.w))
     q = fa.head_norm_rope_kv_write(q_gate, k, v, w["q_norm"], w["k_norm"], k_cache, v_cache,
                                    st.position_start)
-    attn32 = fa.fmha_prefill(q, k_cache[:cache_end], v_cache[:cache_end])
-    attn = fa.output_gate(attn32, q_gate)
+    attn = fa.fmha_prefill_gated(q, k_cache[:cache_end], v_cache[:cache_end], q_gate)
     return pg.linear(attn, w["o_proj"])
 
 

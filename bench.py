@@ -445,6 +445,28 @@ def bench_prefill(torch, fa, dev, t, s, iters, warmup, seed=1):
             "frac_bf16_mfma": tf / BF16_PEAK_TFLOPS}
 
 
+def bench_prefill_gated(torch, fa, dev, t, s, iters, warmup, seed=1):
+    """The prefill attention with the layer's sigmoid output gate: the gate
+    applied in the FMHA launches (bf16 rows out) against the two-launch
+    form (fp32 FMHA rows, then the gate kernel) -- the reference's provider
+    FMHA + full_attention_gate_kernel pair."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(t, 16, 256, generator=gen).to(torch.bfloat16).to(dev)
+    k = torch.randn(s, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+    v = torch.randn(s, 2, 256, generator=gen).to(torch.bfloat16).to(dev)
+    fused_rows = torch.randn(t, 9216, generator=gen).to(torch.bfloat16).to(dev)
+    q_gate = fused_rows[:, :8192]
+    out = torch.empty(t, 4096, dtype=torch.bfloat16, device=dev)
+    a32 = torch.empty(t, 4096, dtype=torch.float32, device=dev)
+    tm = Timer(torch)
+    fused = tm.time(lambda: fa.fmha_prefill_gated(q, k, v, q_gate, out=out), iters, warmup)
+    two = tm.time(lambda: fa.output_gate(fa.fmha_prefill(q, k, v, out=a32), q_gate, out=out),
+                  iters, warmup)
+    flop = PREFILL_FLOP_PER_PAIR * causal_pairs(t, s)
+    return {"q_tokens": t, "kv_tokens": s, "fused_ms": fused, "fmha_then_gate_ms": two,
+            "fused_frac_bf16_mfma": flop / (fused * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+
+
 GDN_STATE_BYTES = 2 * 32 * 128 * 128 * 4     # fp32 state read + write per layer step
 GDN_LAYERS = 30
 
@@ -810,7 +832,9 @@ def run_only(torch, fa, dev, args):
         r = [bench_prefill(torch, fa, dev, 8192, 8192, args.steps, args.warmup),
              bench_prefill(torch, fa, dev, 8192, 12288, args.steps, args.warmup),
              bench_prefill(torch, fa, dev, 1024, 1024, args.steps, args.warmup),
-             bench_prefill(torch, fa, dev, 1024, 5120, args.steps, args.warmup)]
+             bench_prefill(torch, fa, dev, 1024, 5120, args.steps, args.warmup),
+             bench_prefill_gated(torch, fa, dev, 8192, 8192, args.steps, args.warmup),
+             bench_prefill_gated(torch, fa, dev, 1024, 1024, args.steps, args.warmup)]
     elif args.only == "prefill_8k":
         r = bench_prefill(torch, fa, dev, 8192, 8192, args.steps, args.warmup)
     elif args.only == "prefill_c3":
@@ -868,6 +892,8 @@ def main():
                                                                  fused=False),
         "prefill_8k_causal": bench_prefill(torch, fa, dev, 8192, 8192, 10, 2),
         "prefill_8k_over_4k_prefix": bench_prefill(torch, fa, dev, 8192, 12288, 10, 2),
+        "prefill_8k_gated": bench_prefill_gated(torch, fa, dev, 8192, 8192, 10, 2),
+        "prefill_1k_gated": bench_prefill_gated(torch, fa, dev, 1024, 1024, 20, 3),
         "graph_launch_cost": bench_launch_cost(torch, dev),
         "gdn_recurrent_30layers": bench_gdn_recurrent(torch, dev, GDN_LAYERS, 50, 5, use_graph),
         "gdn_fused_gating_update_30layers": bench_gdn_fused_gating_update(torch, dev, GDN_LAYERS,

@@ -63,6 +63,23 @@ size_t qwen36_fmha_prefill_workspace_bytes(unsigned query_tokens, unsigned kv_to
 int qwen36_fmha_prefill(const void* q, const void* k, const void* v, float* out,
                         unsigned query_tokens, unsigned kv_tokens, void* workspace,
                         size_t workspace_bytes, void* stream);
+/* qwen36_fmha_prefill_gated: the attention with the layer's sigmoid output
+ * gate applied in the same launches (the FMHA epilogue, or the split-K
+ * combine), writing bf16 rows instead of fp32 -- the reference runs the
+ * FMHA provider (fp32 out) and then full_attention_gate_kernel's f32 form
+ * (native_full_prefill.hip.cpp:140-266 then native_pointwise.hip.cpp:
+ * 339-359); this is that pair fused, with the gate kernel's roundings
+ * (attention -> bf16, sigmoid -> bf16, product -> bf16), so it equals
+ * qwen36_fmha_prefill followed by qwen36_output_gate bit for bit (a NaN
+ * gate gives a NaN in both).
+ * q_gate: the fused q projection rows [query_tokens][q_gate_row_stride]
+ * bf16 whose head h slice is [q (256) | gate (256)] at h*512 (stride >=
+ * 8192, 8-byte aligned); out [query_tokens, 4096] bf16, 16-byte aligned.
+ * Workspace as qwen36_fmha_prefill (same size function). */
+int qwen36_fmha_prefill_gated(const void* q, const void* k, const void* v,
+                              const void* q_gate, unsigned q_gate_row_stride, void* out,
+                              unsigned query_tokens, unsigned kv_tokens, void* workspace,
+                              size_t workspace_bytes, void* stream);
 /* Legacy fixed-shape q8192 exports (qrt_ck_fmha_q8192_provider.cpp:214-300).
  * qrt_ck_fmha_q8192_f32_launch (:228-271): packed_qkv fp32 [8192, 9216] rows
  * of [q (4096) | 4096 more q_proj features, unused | k (512) | v (512)],

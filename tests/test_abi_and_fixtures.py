@@ -57,6 +57,14 @@ def test_bad_arguments_rejected_without_launch(lib):
     assert L.qrt_ck_fmha_bf16_launch(None, None, None, None, 16, None) == 1
     assert L.qrt_ck_fmha_bf16_launch_ex(1, 1, 1, 1, 8, 4, None) == 1
     assert L.qrt_ck_fmha_bf16_launch_ex(1, 1, 1, 1, 8, 262145, None) == 1
+    # gated FMHA: null gate, short gate stride, misaligned gate / output
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, None, 9216, 16, 8, 8, None, 0, None) == 1
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, 16, 4096, 16, 8, 8, None, 0, None) == 1
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, 18, 9216, 16, 8, 8, None, 0, None) == 1
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, 16, 9216, 24, 8, 8, None, 0, None) == 1
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, 16, 9216, 16, 8, 4, None, 0, None) == 1
+    # short prompt without its split workspace
+    assert L.qwen36_fmha_prefill_gated(16, 16, 16, 16, 9216, 16, 1024, 1024, None, 0, None) == 1
     assert L.qwen36_decode_gqa(None, None, None, None, None, 0, 1, 1, None, 0, None, None, 0, 0, None) == 1
     # cache_end beyond capacity
     assert L.qwen36_decode_gqa(1, None, None, 1, 1, 0, 9, 8, None, 0, 1, 1, 1 << 20, 0, None) == 1

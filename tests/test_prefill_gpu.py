@@ -222,7 +222,8 @@ def test_config3_norm_rope_kv_write_and_gated_output(gpu):
     write_kv_cache (V bit-exact, K to the bf16 bar with >= 99% bit-equal),
     the gated output on sampled rows vs the oracle's SDPA + output_gate
     (fle:5151-5162, 5980-5986, 6627-6650)."""
-    from qwen36_attn.full_attention import fmha_prefill, head_norm_rope_kv_write, output_gate
+    from qwen36_attn.full_attention import (fmha_prefill, fmha_prefill_gated,
+                                            head_norm_rope_kv_write, output_gate)
     from qwen36_attn import synthetic as syn
     t, pre = 8192, 4096
     s = pre + t
@@ -241,7 +242,10 @@ def test_config3_norm_rope_kv_write_and_gated_output(gpu):
     qgd = qg.to(gpu)
     q = head_norm_rope_kv_write(qgd, kn.to(gpu), vn.to(gpu), qw.to(gpu), kw.to(gpu), kcd, vcd, pre)
     attn32 = fmha_prefill(q, kcd, vcd)
-    gated = output_gate(attn32, qgd).cpu()
+    gated_d = output_gate(attn32, qgd)
+    # the fused form (gate in the FMHA epilogue) is the same bits
+    assert torch.equal(fmha_prefill_gated(q, kcd, vcd, qgd), gated_d)
+    gated = gated_d.cpu()
     kcg, vcg, qh = kcd.cpu(), vcd.cpu(), q.cpu()
     # oracle: the same three steps on the CPU
     cos, sin = O.rope_cos_sin(pre, t)
@@ -263,6 +267,51 @@ def test_config3_norm_rope_kv_write_and_gated_output(gpu):
         a = O.prefill_attention(qh[r:r + 1], kc[:lim], vc[:lim], lim - 1, out_dtype=torch.float32)
         ref = O.output_gate(a.to(torch.bfloat16), gate_ref[r:r + 1])
         assert (gated[r:r + 1].float() - ref.float()).abs().max().item() <= TOL, r
+
+
+@pytest.mark.parametrize("t,s", [(1, 1), (300, 300), (1024, 1024), (100, 4196), (4096, 4096),
+                                 (2048, 6144)])
+def test_gated_prefill_equals_fmha_then_gate(gpu, t, s):
+    """The gate applied in the FMHA epilogue (unsplit) or in the split-K
+    combine equals the two-launch path -- fp32 FMHA rows, then the gate
+    kernel -- bit for bit, with the gate read through the [T, 9216] fused
+    projection rows' column view."""
+    from qwen36_attn.full_attention import fmha_prefill, fmha_prefill_gated, output_gate
+    q, k, v = _inputs(t, s, seed=t + 3 * s)
+    g = torch.Generator().manual_seed(t)
+    fused = (torch.randn(t, 9216, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    q_gate = fused[:, :8192]
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    print(f"gated prefill T={t} S={s}", flush=True)
+    two = output_gate(fmha_prefill(qd, kd, vd), q_gate)
+    one = fmha_prefill_gated(qd, kd, vd, q_gate)
+    torch.cuda.synchronize()
+    assert torch.equal(one, two)
+    assert one.shape == (t, 4096) and one.dtype == torch.bfloat16
+
+
+@pytest.mark.parametrize("t", [16, 4096])
+def test_gated_prefill_every_gate_value(gpu, t):
+    """Every one of the 65536 bf16 gate bit patterns (infinities,
+    subnormals, zeros of both signs included) through the fused gate --
+    the split combine (T = 16) and the FMHA epilogue (T = 4096) -- gives the
+    gate kernel's bits exactly (compared as bit patterns); a NaN gate gives
+    a NaN in both (its sign and payload are not part of the contract)."""
+    from qwen36_attn.full_attention import fmha_prefill, fmha_prefill_gated, output_gate
+    q, k, v = _inputs(t, t, seed=77 + t)
+    pats = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(16, 4096)
+    gate = pats.repeat((t + 15) // 16, 1)[:t].view(torch.bfloat16)
+    qg = torch.zeros(t, 8192, dtype=torch.bfloat16)
+    qg.view(t, 16, 512)[:, :, 256:] = gate.view(t, 16, 256)
+    qd, kd, vd, qgd = q.to(gpu), k.to(gpu), v.to(gpu), qg.to(gpu)
+    print(f"gated prefill, all gate values, T={t}", flush=True)
+    two = output_gate(fmha_prefill(qd, kd, vd), qgd)
+    one = fmha_prefill_gated(qd, kd, vd, qgd)
+    torch.cuda.synchronize()
+    nan = torch.isnan(two)
+    assert torch.equal(torch.isnan(one), nan)
+    assert torch.equal(one.view(torch.int16)[~nan], two.view(torch.int16)[~nan])
+    assert nan.sum().item() == 254 * t * 4096 // 65536   # the NaN patterns only
 
 
 def test_split_prefill_ignores_stale_workspace(gpu):
