@@ -52,6 +52,10 @@ constexpr int kGdnConvK = 4;
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+__host__ __forceinline__ bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
 __device__ __forceinline__ float bf2f(bf16 x) { return (float)x; }
 __device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }  // RNE
 
@@ -63,6 +67,24 @@ __device__ __forceinline__ bf16 gate_bf16(float attn, bf16 gate) {
   const bf16 a = f2bf(attn);
   const bf16 sg = f2bf(1.0f / (1.0f + expf(-bf2f(gate))));
   return f2bf(__fmul_rn(bf2f(a), bf2f(sg)));
+}
+
+// log2(e) split for exp2 arguments: g * kLog2eHi is exact for bf16 g.
+constexpr float kLog2eHi = 1.44268798828125f;       // 47274 / 2^15
+constexpr float kLn2Lo = 4.888495152129525e-06f;    // (log2(e) - kLog2eHi) ln 2
+
+// x / (1 + e^-x) (SiLU as the reference's conv writes it) for a bf16 x,
+// from the hardware exp2 and reciprocal with the split log2(e) of
+// gate4_bf16_fast: within ~5 ulps of the exact form's value.  Sets `slow`
+// when that value could round to another bf16 than the exact one (within
+// 32 ulps of a rounding midpoint), or |x| > 60, or x is not finite.
+__device__ __forceinline__ float silu_fast(float x, bool& slow) {
+  const float th = __builtin_amdgcn_exp2f(x * -kLog2eHi);
+  const float t = __builtin_fmaf(th, x * -kLn2Lo, th);
+  const float s = x * __builtin_amdgcn_rcpf(1.0f + t);
+  const int mid = (int)(__float_as_uint(s) & 0xffffu) - 0x8000;
+  slow = !(fabsf(x) <= 60.0f) || (mid >= -32 && mid <= 32);
+  return s;
 }
 
 // gate_bf16 for four values, with the sigmoid from the hardware exp2 and
@@ -77,8 +99,6 @@ __device__ __forceinline__ bf16 gate_bf16(float attn, bf16 gate) {
 // 65536 bf16 gates; a NaN gate gives a NaN) at a fraction of the
 // instructions -- for epilogues, where the gate's math is not spread over a
 // whole elementwise launch.
-constexpr float kLog2eHi = 1.44268798828125f;       // 47274 / 2^15
-constexpr float kLn2Lo = 4.888495152129525e-06f;    // (log2(e) - kLog2eHi) ln 2
 __device__ __forceinline__ bf16x4 gate4_bf16_fast(const f32x4& attn, const bf16x4& gate) {
   float sg[4];
   bool slow = false;
@@ -172,11 +192,11 @@ __device__ __forceinline__ void rope_cos_sin_wave(unsigned pos, const float* inv
 // lanes 8-15).
 // Returns the fp32 values before the final bf16 rounding.
 // (four_layer_mini_engine.py:5151-5162; native_pointwise.hip.cpp:242-337.)
-__device__ __forceinline__ void head_norm_rope_wave(const float (&x)[4],
-                                                    const bf16* __restrict__ w,
-                                                    const float (&cs)[4],
-                                                    const float (&sn)[4],
-                                                    float (&y)[4]) {
+__device__ __forceinline__ void head_norm_rope_wave_wp1(const float (&x)[4],
+                                                        const float (&wp1)[4],
+                                                        const float (&cs)[4],
+                                                        const float (&sn)[4],
+                                                        float (&y)[4]) {
   const int lane = threadIdx.x & 63;
   float sq[4];
 #pragma unroll
@@ -187,10 +207,7 @@ __device__ __forceinline__ void head_norm_rope_wave(const float (&x)[4],
   const float var = __fmul_rn(sum, 1.0f / 256.0f);
   const float inv = (float)(1.0 / sqrt((double)__fadd_rn(var, 1e-6f)));
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float wp1 = __fadd_rn(bf2f(w[4 * lane + e]), 1.0f);
-    y[e] = bf2f(f2bf(__fmul_rn(__fmul_rn(x[e], inv), wp1)));
-  }
+  for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(__fmul_rn(__fmul_rn(x[e], inv), wp1[e])));
   float mate[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) mate[e] = __shfl_xor(y[e], 8, 64);
@@ -200,6 +217,23 @@ __device__ __forceinline__ void head_norm_rope_wave(const float (&x)[4],
       y[e] = lane < 8 ? __fsub_rn(__fmul_rn(y[e], cs[e]), __fmul_rn(mate[e], sn[e]))
                       : __fadd_rn(__fmul_rn(y[e], cs[e]), __fmul_rn(mate[e], sn[e]));
   }
+}
+
+// The (w + 1) factors of this lane's four dims.
+__device__ __forceinline__ void head_norm_wp1(const bf16* __restrict__ w, float (&wp1)[4]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) wp1[e] = __fadd_rn(bf2f(w[4 * lane + e]), 1.0f);
+}
+
+__device__ __forceinline__ void head_norm_rope_wave(const float (&x)[4],
+                                                    const bf16* __restrict__ w,
+                                                    const float (&cs)[4],
+                                                    const float (&sn)[4],
+                                                    float (&y)[4]) {
+  float wp1[4];
+  head_norm_wp1(w, wp1);
+  head_norm_rope_wave_wp1(x, wp1, cs, sn, y);
 }
 
 }  // namespace q36

@@ -60,9 +60,6 @@ constexpr int kC = 64;
 constexpr unsigned kFlagQkNormalized = 1u;   // q, k already l2-normalised
 constexpr unsigned kFlagStateVk = 2u;        // states in [Hv, dv, dk] order
 
-__host__ __forceinline__ bool aligned16(const void* p) {
-  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
-}
 constexpr int kPitchR = 136;   // bf16 row pitch (272 B) of [64][128] tiles
 constexpr int kPitchF = 68;    // fp32 row pitch of [64][64] matrices
 constexpr float kQScale = 0.08838834764831845f;   // 1/sqrt(128)

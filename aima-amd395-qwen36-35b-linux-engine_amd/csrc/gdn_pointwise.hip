@@ -66,6 +66,108 @@ __global__ __launch_bounds__(256) void gdn_conv1d_kernel(
   }
 }
 
+// Vector form of gdn_conv1d_kernel (16-byte loads and stores, the same
+// conv arithmetic; SiLU through silu_fast with the exact form where it could
+// differ, so the same bits for every finite input): grid = (C/2048, ceil(T/16));
+// thread = 8 consecutive channels, 16 consecutive tokens, whose input rows
+// are all requested before the first output is formed.
+__global__ __launch_bounds__(256) void gdn_conv1d_vec_kernel(
+    const bf16* __restrict__ x, unsigned x_row_stride,
+    const bf16* __restrict__ weight, const bf16* __restrict__ state_in,
+    bf16* __restrict__ state_out, bf16* __restrict__ out, unsigned tokens) {
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  const unsigned t0 = blockIdx.y * kConvTokensPerThread;
+  float w[8][kGdnConvK];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16x8 wv = *reinterpret_cast<const bf16x8*>(weight + c0 * kGdnConvK + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[2 * i + e / 4][e % 4] = bf2f(wv[e]);
+  }
+  // window rows t0-3 .. t0-1 (from the state before the first token), then
+  // the block's 16 rows (rows past the end re-read the last row, not stored)
+  bf16x8 rows[3 + kConvTokensPerThread];
+  bf16 st[24] = {};
+  if (blockIdx.y == 0) {   // only the first token block reads the state
+    const bf16x8* sp = reinterpret_cast<const bf16x8*>(state_in + c0 * 3);
+    const bf16x8 a = sp[0], b = sp[1], c = sp[2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      st[e] = a[e];
+      st[8 + e] = b[e];
+      st[16 + e] = c[e];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 3 + kConvTokensPerThread; ++j) {
+    const int tok = (int)t0 - 3 + j;
+    if (tok >= 0) {
+      const unsigned tc = min((unsigned)tok, tokens - 1);
+      rows[j] = *reinterpret_cast<const bf16x8*>(x + (size_t)tc * x_row_stride + c0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) rows[j][e] = st[e * 3 + (tok + 3)];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kConvTokensPerThread; ++j) {
+    const unsigned t = t0 + j;
+    // SiLU from the hardware exp2 / rcp; the exact form only where the fast
+    // value could round to another bf16 (one branch per row of 8)
+    float cv[8], sv[8];
+    bool slow = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = mul_rn(bf2f(rows[j][e]), w[e][0]);
+      acc = add_rn(acc, mul_rn(bf2f(rows[j + 1][e]), w[e][1]));
+      acc = add_rn(acc, mul_rn(bf2f(rows[j + 2][e]), w[e][2]));
+      acc = add_rn(acc, mul_rn(bf2f(rows[j + 3][e]), w[e][3]));
+      cv[e] = bf2f(f2bf(acc));
+      bool sl;
+      sv[e] = silu_fast(cv[e], sl);
+      slow |= sl;
+    }
+    if (slow) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        bool sl;
+        silu_fast(cv[e], sl);
+        if (sl) sv[e] = cv[e] / (1.0f + expf(-cv[e]));
+      }
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = f2bf(sv[e]);
+    if (t < tokens) *reinterpret_cast<bf16x8*>(out + (size_t)t * kGdnConvDim + c0) = o;
+  }
+  // The first token block owns the state update (state_in may alias
+  // state_out: this thread read its state above).
+  if (blockIdx.y == 0) {
+    bf16 ns[24];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int tok = (int)tokens - 3 + j;
+      bf16x8 r;
+      if (tok >= 0) {
+        r = *reinterpret_cast<const bf16x8*>(x + (size_t)tok * x_row_stride + c0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) r[e] = st[e * 3 + (tok + 3)];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ns[e * 3 + j] = r[e];
+    }
+    bf16x8* dp = reinterpret_cast<bf16x8*>(state_out + c0 * 3);
+#pragma unroll
+    for (int v8 = 0; v8 < 3; ++v8) {
+      bf16x8 r;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = ns[8 * v8 + e];
+      dp[v8] = r;
+    }
+  }
+}
+
 __global__ void gdn_gating_kernel(const bf16* __restrict__ a,
                                   const bf16* __restrict__ b,
                                   unsigned ab_row_stride,
@@ -113,6 +215,48 @@ __global__ __launch_bounds__(256) void gdn_gated_norm_kernel(
   }
 }
 
+// Vector form of gdn_gated_norm_kernel: thread = 8 dims of one (token,
+// v-head) row, 16 threads per row, 16 rows per block; 16-byte loads and
+// stores.  The sum of squares is reduced in the scalar kernel's exact order
+// (its lane 4s + i holds this thread's pair i; its xor-32 .. xor-4 steps
+// are xor 8 .. 1 here, its xor-2 and xor-1 steps pair the thread's own
+// partials), so the bits are the same.
+__global__ __launch_bounds__(256) void gdn_gated_norm_vec_kernel(
+    const bf16* __restrict__ core, const bf16* __restrict__ z,
+    unsigned z_row_stride, const bf16* __restrict__ weight,
+    bf16* __restrict__ out, unsigned rows) {
+  const unsigned row = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const bool live = row < rows;
+  const unsigned rr = live ? row : rows - 1;
+  const unsigned t = rr / kGdnHv, h = rr % kGdnHv;
+  const bf16x8 xv = *reinterpret_cast<const bf16x8*>(core + (size_t)rr * kGdnDv + 8 * sub);
+  const bf16x8 zv = *reinterpret_cast<const bf16x8*>(z + (size_t)t * z_row_stride + h * kGdnDv + 8 * sub);
+  const bf16x8 wv = *reinterpret_cast<const bf16x8*>(weight + 8 * sub);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x0 = bf2f(xv[2 * i]), x1 = bf2f(xv[2 * i + 1]);
+    p[i] = add_rn(mul_rn(x0, x0), mul_rn(x1, x1));
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = add_rn(p[i], __shfl_xor(p[i], o, 16));
+  const float sum = add_rn(add_rn(p[0], p[2]), add_rn(p[1], p[3]));
+  const float inv = rsqrt_rn(add_rn(mul_rn(sum, 1.0f / 128.0f), 1e-6f));
+  bf16x8 o8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float nv = bf2f(f2bf(mul_rn(mul_rn(bf2f(xv[e]), inv), bf2f(wv[e]))));
+    const float zf = bf2f(zv[e]);
+    const float silu = zf / (1.0f + expf(-zf));
+    o8[e] = f2bf(mul_rn(nv, silu));
+  }
+  if (live)
+    *reinterpret_cast<bf16x8*>(out + (size_t)t * (kGdnHv * kGdnDv) + h * kGdnDv + 8 * sub) = o8;
+}
+
 }  // namespace
 }  // namespace q36
 
@@ -126,8 +270,18 @@ Q36_EXPORT int qwen36_gdn_conv1d(const void* x, unsigned x_row_stride,
       state_out == nullptr || out == nullptr || tokens == 0 ||
       tokens > kMaxTokens || x_row_stride < (unsigned)kGdnConvDim)
     return Q36_EINVAL;
-  const dim3 grid(kGdnConvDim / 256,
-                  (tokens + kConvTokensPerThread - 1) / kConvTokensPerThread);
+  const unsigned tblocks = (tokens + kConvTokensPerThread - 1) / kConvTokensPerThread;
+  const bool vec = aligned16(x) && aligned16(weight) && aligned16(state_in) &&
+                   aligned16(state_out) && aligned16(out) && (x_row_stride % 8) == 0;
+  if (vec) {
+    hipLaunchKernelGGL(gdn_conv1d_vec_kernel, dim3(kGdnConvDim / 2048, tblocks), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16*>(x),
+                       x_row_stride, static_cast<const bf16*>(weight),
+                       static_cast<const bf16*>(state_in), static_cast<bf16*>(state_out),
+                       static_cast<bf16*>(out), tokens);
+    return static_cast<int>(hipGetLastError());
+  }
+  const dim3 grid(kGdnConvDim / 256, tblocks);
   hipLaunchKernelGGL(gdn_conv1d_kernel, grid, dim3(256), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const bf16*>(x), x_row_stride,
@@ -165,6 +319,14 @@ Q36_EXPORT int qwen36_gdn_gated_norm(const void* core, const void* z,
       z_row_stride < (unsigned)(kGdnHv * kGdnDv))
     return Q36_EINVAL;
   const unsigned rows = tokens * kGdnHv;
+  if (aligned16(core) && aligned16(z) && aligned16(weight) && aligned16(out) &&
+      (z_row_stride % 8) == 0) {
+    hipLaunchKernelGGL(gdn_gated_norm_vec_kernel, dim3((rows + 15) / 16), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16*>(core),
+                       static_cast<const bf16*>(z), z_row_stride,
+                       static_cast<const bf16*>(weight), static_cast<bf16*>(out), rows);
+    return static_cast<int>(hipGetLastError());
+  }
   hipLaunchKernelGGL(gdn_gated_norm_kernel, dim3((rows + 3) / 4), dim3(256), 0,
                      static_cast<hipStream_t>(stream),
                      static_cast<const bf16*>(core), static_cast<const bf16*>(z),

@@ -638,8 +638,6 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   *reinterpret_cast<bf16x8*>(out + (size_t)t * kMoeHidden + c) = o;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) % 16) == 0; }
-
 }  // namespace
 }  // namespace q36
 

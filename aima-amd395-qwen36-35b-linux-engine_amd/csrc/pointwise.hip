@@ -74,6 +74,52 @@ __global__ __launch_bounds__(64) void head_norm_rope_kernel(
   }
 }
 
+// One wave per token (block = 4 tokens): the token's 16 query heads and 2
+// key heads through the same per-head arithmetic as head_norm_rope_kernel,
+// with the RoPE cos/sin and the (w + 1) factors formed once per wave and
+// every input row requested up front (8-byte pieces per lane).
+__global__ __launch_bounds__(256) void head_norm_rope_rows_kernel(
+    const bf16* __restrict__ q_gate, unsigned q_row_stride,
+    const bf16* __restrict__ k_raw, unsigned k_row_stride,
+    const bf16* __restrict__ v_raw, unsigned v_row_stride,
+    const bf16* __restrict__ q_weight, const bf16* __restrict__ k_weight,
+    unsigned position_start, bf16* __restrict__ q_out,
+    bf16* __restrict__ k_cache, bf16* __restrict__ v_cache, unsigned tokens) {
+  const unsigned t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;   // wave-uniform
+  const int lane = threadIdx.x & 63;
+  bf16x4 xin[kHq + kHkv], vin[kHkv];
+#pragma unroll
+  for (int h = 0; h < kHq; ++h)
+    xin[h] = *reinterpret_cast<const bf16x4*>(q_gate + (size_t)t * q_row_stride + h * 2 * kD + 4 * lane);
+#pragma unroll
+  for (int h = 0; h < kHkv; ++h) {
+    xin[kHq + h] = *reinterpret_cast<const bf16x4*>(k_raw + (size_t)t * k_row_stride + h * kD + 4 * lane);
+    vin[h] = *reinterpret_cast<const bf16x4*>(v_raw + (size_t)t * v_row_stride + h * kD + 4 * lane);
+  }
+  float wq[4], wk[4], cs[4], sn[4];
+  head_norm_wp1(q_weight, wq);
+  head_norm_wp1(k_weight, wk);
+  rope_cos_sin_wave(position_start + t, c_inv_freq, cs, sn);
+  const size_t pos = position_start + t;
+#pragma unroll
+  for (int h = 0; h < kHq + kHkv; ++h) {
+    float x[4], y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = bf2f(xin[h][e]);
+    head_norm_rope_wave_wp1(x, h < kHq ? wq : wk, cs, sn, y);
+    bf16x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f2bf(y[e]);
+    bf16* dst = h < kHq ? q_out + ((size_t)t * kHq + h) * kD
+                        : k_cache + (pos * kHkv + (h - kHq)) * kD;
+    *reinterpret_cast<bf16x4*>(dst + 4 * lane) = o;
+  }
+#pragma unroll
+  for (int h = 0; h < kHkv; ++h)
+    *reinterpret_cast<bf16x4*>(v_cache + (pos * kHkv + h) * kD + 4 * lane) = vin[h];
+}
+
 template <bool kF32>
 __global__ void output_gate_kernel(const void* __restrict__ attn,
                                    const bf16* __restrict__ q_gate,
@@ -139,6 +185,18 @@ Q36_EXPORT int qwen36_head_norm_rope(
     return Q36_EINVAL;
   const int st = ensure_inv_freq();
   if (st != Q36_OK) return st;
+  const auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
+  if (a8(q_gate) && a8(k_raw) && a8(v_raw) && a8(q_out) && a8(k_cache) && a8(v_cache) &&
+      (q_row_stride % 4) == 0 && (k_row_stride % 4) == 0 && (v_row_stride % 4) == 0) {
+    hipLaunchKernelGGL(head_norm_rope_rows_kernel, dim3((tokens + 3) / 4), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const bf16*>(q_gate),
+                       q_row_stride, static_cast<const bf16*>(k_raw), k_row_stride,
+                       static_cast<const bf16*>(v_raw), v_row_stride,
+                       static_cast<const bf16*>(q_weight), static_cast<const bf16*>(k_weight),
+                       position_start, static_cast<bf16*>(q_out), static_cast<bf16*>(k_cache),
+                       static_cast<bf16*>(v_cache), tokens);
+    return static_cast<int>(hipGetLastError());
+  }
   hipLaunchKernelGGL(head_norm_rope_kernel, dim3(tokens, kHq + kHkv), dim3(64),
                      0, static_cast<hipStream_t>(stream),
                      static_cast<const bf16*>(q_gate), q_row_stride,

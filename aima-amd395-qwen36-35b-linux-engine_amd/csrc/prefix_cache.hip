@@ -132,8 +132,6 @@ int launch_copy(Pool& p, Entry& e, unsigned long long tokens, bool to_snapshot,
   return static_cast<int>(hipGetLastError());
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
 }  // namespace
 }  // namespace q36
 

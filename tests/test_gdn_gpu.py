@@ -126,6 +126,62 @@ def test_config4_prefill_then_decode(gpu):
     assert rel_err(st.cpu(), ref_s2) <= TOL_STATE
 
 
+@pytest.mark.parametrize("t", [1, 2, 3, 17, 300, 1000])
+def test_vector_pointwise_kernels_match_scalar_forms(gpu, t):
+    """The 16-byte conv and gated-norm kernels (aligned inputs) give the
+    scalar kernels' bits (the same inputs through an odd-strided view, which
+    the library routes to the scalar forms)."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(40 + t)
+    x = syn.randn((t, 8192), g)
+    w = syn.randn((8192, 4), g, 0.5)
+    st = syn.randn((8192, 3), g)
+    xd = x.to(gpu)
+    wide = torch.zeros(t, 8193, dtype=torch.bfloat16, device=gpu)
+    wide[:, 1:] = xd
+    print(f"conv / gated norm vector vs scalar T={t}", flush=True)
+    out_v, st_v = G.causal_conv1d(xd, st.to(gpu), w.to(gpu))
+    out_s, st_s = G.causal_conv1d(wide[:, 1:], st.to(gpu), w.to(gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(out_v, out_s) and torch.equal(st_v, st_s)
+    core = syn.randn((t, 32, 128), g).to(gpu)
+    z = syn.randn((t, 4096), g).to(gpu)
+    zw = torch.zeros(t, 4097, dtype=torch.bfloat16, device=gpu)
+    zw[:, 1:] = z
+    wn = syn.randn((128,), g, 0.5).to(gpu)
+    n_v = G.gated_rmsnorm(core, z, wn)
+    n_s = G.gated_rmsnorm(core, zw[:, 1:], wn)
+    torch.cuda.synchronize()
+    assert torch.equal(n_v, n_s)
+
+
+def test_vector_conv_silu_every_input_value(gpu):
+    """The vector conv's SiLU (hardware exp2 / rcp with the exact form near
+    bf16 rounding midpoints) against the scalar kernel's exact form for all
+    65536 bf16 conv values: taps (0, 0, 0, 1) make the conv value the input
+    itself on every fourth row (the rows between are zero; non-finite inputs
+    make NaNs there in both kernels)."""
+    from qwen36_attn import gated_deltanet as G
+    pats = torch.arange(-32768, 32768, dtype=torch.int32).to(torch.int16).view(8, 8192)
+    x = torch.zeros(32, 8192, dtype=torch.bfloat16)
+    x[0::4] = pats.view(torch.bfloat16)
+    w = torch.zeros(8192, 4, dtype=torch.bfloat16)
+    w[:, 3] = 1.0
+    st = torch.zeros(8192, 3, dtype=torch.bfloat16)
+    xd = x.to(gpu)
+    wide = torch.zeros(32, 8193, dtype=torch.bfloat16, device=gpu)
+    wide[:, 1:] = xd
+    print("conv SiLU over all bf16 inputs", flush=True)
+    out_v, _ = G.causal_conv1d(xd, st.to(gpu), w.to(gpu))
+    out_s, _ = G.causal_conv1d(wide[:, 1:], st.to(gpu), w.to(gpu))
+    torch.cuda.synchronize()
+    nan = torch.isnan(out_s)
+    assert torch.equal(torch.isnan(out_v), nan)
+    assert torch.equal(out_v.view(torch.int16)[~nan], out_s.view(torch.int16)[~nan])
+    # NaN conv values only from the 254 NaN inputs and -inf (-inf / inf)
+    assert nan[0::4].sum().item() == 255
+
+
 def test_conv1d_gating_norm(gpu):
     from qwen36_attn import gated_deltanet as G
     g = syn.gen(11)

@@ -314,6 +314,32 @@ def test_gated_prefill_every_gate_value(gpu, t):
     assert nan.sum().item() == 254 * t * 4096 // 65536   # the NaN patterns only
 
 
+@pytest.mark.parametrize("t,pos", [(1, 0), (5, 4093), (300, 0), (1000, 123457)])
+def test_head_norm_rope_rows_kernel_matches_per_head_form(gpu, t, pos):
+    """The one-wave-per-token head norm + RoPE kernel (8-byte aligned rows)
+    gives the per-(token, head) kernel's bits (the same rows through an
+    odd-strided view, which the library routes to that form): q, the
+    normalised K rows and the raw V rows in the caches."""
+    from qwen36_attn.full_attention import head_norm_rope_kv_write
+    from qwen36_attn import synthetic as syn
+    g = syn.gen(60 + t)
+    qg = syn.randn((t, 8192), g).to(gpu)
+    kr = syn.randn((t, 512), g).to(gpu)
+    vr = syn.randn((t, 512), g).to(gpu)
+    qw = syn.randn((256,), g, 0.1).to(gpu)
+    kw = syn.randn((256,), g, 0.1).to(gpu)
+    wide = torch.zeros(t, 8193, dtype=torch.bfloat16, device=gpu)
+    wide[:, 1:] = qg
+    cap = pos + t
+    caches = [torch.zeros(cap, 2, 256, dtype=torch.bfloat16, device=gpu) for _ in range(4)]
+    print(f"head norm rope rows vs per-head T={t} pos={pos}", flush=True)
+    q1 = head_norm_rope_kv_write(qg, kr, vr, qw, kw, caches[0], caches[1], pos)
+    q2 = head_norm_rope_kv_write(wide[:, 1:], kr, vr, qw, kw, caches[2], caches[3], pos)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2)
+    assert torch.equal(caches[0], caches[2]) and torch.equal(caches[1], caches[3])
+
+
 def test_split_prefill_ignores_stale_workspace(gpu):
     """A short prompt (split key ranges + combine through the shared scratch)
     does not depend on what the scratch held before the call: NaN-filled
