@@ -908,6 +908,7 @@ def main():
                                                              use_graph, fused=False),
         "gdn_chunk_prefill_8k": bench_gdn_prefill(torch, dev, 8192, 10, 2),
         "config1_layers_1k": bench_config1_layers(torch, dev, 1024, 20, 3),
+        "prefill_layers_8k": bench_config1_layers(torch, dev, 8192, 10, 2),
         "config1_sequence": bench_config1_sequence(torch, dev),
         "prefill_projections_1k": bench_prefill_projections(torch, dev, 1024, 20, 3),
         "prefill_projections_1k_torch": bench_prefill_projections(torch, dev, 1024, 20, 3,
