@@ -740,11 +740,12 @@ def _median_time(fn, min_runs=3, budget_s=8.0, max_runs=20):
     return times[len(times) // 2], len(times)
 
 
-def cpu_prefill_baseline(torch, rows=256):
+def cpu_prefill_baseline(torch, rows=8192):
     """Config 3 on this host's cores: the oracle's SDPA (fp32 evaluation of
     the bf16 inputs, as the FMHA provider returns fp32) for the last ``rows``
-    query rows of the 8192-token block over the 12288-row cache (the rows
-    with the most keys), scaled to the whole block by unmasked (q, k) pairs."""
+    query rows of the 8192-token block over the 12288-row cache (the whole
+    block by default; fewer rows are the ones with the most keys, scaled to
+    the whole block by unmasked (q, k) pairs)."""
     from oracle import attention_oracle as O
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -757,18 +758,20 @@ def cpu_prefill_baseline(torch, rows=256):
     scale = causal_pairs(t_full, s_full) / causal_pairs(rows, s_full)
     ms = med * scale * 1e3
     flop = PREFILL_FLOP_PER_PAIR * causal_pairs(t_full, s_full)
+    what = (f"the whole block ({t_full} query rows x {s_full} keys)" if rows == t_full else
+            f"the last {rows} query rows x {s_full} keys, scaled x{scale:.1f} by unmasked pairs to "
+            f"8192 rows over a 4096-token prefix")
     return {"value": ms, "unit": "ms", "tflops": flop / (ms * 1e-3) / 1e12, "cores": threads,
             "kind": "port",
-            "sample": f"median of {n} oracle SDPA runs (torch CPU fp32, {_cpu_info()}) over the last "
-                      f"{rows} query rows x {s_full} keys, scaled x{scale:.1f} by unmasked pairs to "
-                      f"8192 rows over a 4096-token prefix"}
+            "sample": f"median of {n} oracle SDPA runs (torch CPU fp32, {_cpu_info()}) over {what}"}
 
 
-def cpu_gdn_baseline(torch, chunk_tokens=512, steps=8):
+def cpu_gdn_baseline(torch, chunk_tokens=8192, steps=64):
     """Config 4 on this host's cores: the oracle's chunked delta rule
-    (fp32, chunk 64, 32 v-heads) over ``chunk_tokens`` tokens scaled
-    linearly (the chunk loop is sequential and every chunk costs the same)
-    to 8192, plus ``steps`` recurrent steps scaled to 64."""
+    (fp32, chunk 64, 32 v-heads) over ``chunk_tokens`` tokens (the whole
+    8192 by default; fewer are scaled linearly -- the chunk loop is
+    sequential and every chunk costs the same), plus ``steps`` recurrent
+    steps (config 4's 64 by default), reported per step."""
     from oracle import attention_oracle as O
     from qwen36_attn import synthetic as syn
     threads = len(os.sched_getaffinity(0))
@@ -789,8 +792,9 @@ def cpu_gdn_baseline(torch, chunk_tokens=512, steps=8):
     flop, _ = gdn_prefill_work(8192)
     return {"prefill_8k_ms": prefill_ms, "prefill_tflops": flop / (prefill_ms * 1e-3) / 1e12,
             "recurrent_us_per_step": decode_us, "cores": threads, "kind": "port",
-            "sample": f"median of {n_c} oracle chunked-rule runs over {c} tokens scaled x{8192 // c} "
-                      f"to 8192, median of {n_r} runs of {steps} recurrent steps (torch CPU fp32, "
+            "sample": f"median of {n_c} oracle chunked-rule runs over {c} tokens"
+                      + (f" scaled x{8192 // c} to 8192" if c != 8192 else "")
+                      + f", median of {n_r} runs of {steps} recurrent steps (torch CPU fp32, "
                       f"{_cpu_info()})"}
 
 
