@@ -270,7 +270,7 @@ def test_config3_norm_rope_kv_write_and_gated_output(gpu):
 
 
 @pytest.mark.parametrize("t,s", [(1, 1), (300, 300), (1024, 1024), (100, 4196), (4096, 4096),
-                                 (2048, 6144)])
+                                 (2048, 6144), (4000, 4000), (3900, 5000)])
 def test_gated_prefill_equals_fmha_then_gate(gpu, t, s):
     """The gate applied in the FMHA epilogue (unsplit) or in the split-K
     combine equals the two-launch path -- fp32 FMHA rows, then the gate
