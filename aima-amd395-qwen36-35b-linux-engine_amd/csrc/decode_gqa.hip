@@ -400,11 +400,6 @@ __global__ __launch_bounds__(64) void decode_gqa_combine_wave_kernel(
   constexpr int kPer = kMaxSplits / 16;   // at most 16 splits per group
   float2 ml[kPer];
   f32x4 os[kPer];
-  float gv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (gate != nullptr && sg == 0) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) gv[e] = bf2f(gate[(size_t)head * gate_head_stride + d0 + e]);
-  }
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const unsigned sp = sg + 16 * u;
@@ -415,6 +410,13 @@ __global__ __launch_bounds__(64) void decode_gqa_combine_wave_kernel(
       ml[u] = float2{-INFINITY, 0.f};
       os[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+  // the gate is requested after the partials (and every lane reads it, kept
+  // as raw bits), so its load joins their round trip instead of preceding it
+  bf16 graw[4] = {};
+  if (gate != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) graw[e] = gate[(size_t)head * gate_head_stride + d0 + e];
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(64) void decode_gqa_combine_wave_kernel(
     for (int e = 0; e < 4; ++e) {
       bf16 x = f2bf(acc[e] / L);
       if (gate != nullptr) {
-        const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-gv[e])));
+        const bf16 sg_b = f2bf(1.0f / (1.0f + expf(-bf2f(graw[e]))));
         x = f2bf(bf2f(x) * bf2f(sg_b));
       }
       ob[e] = x;
