@@ -42,17 +42,21 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
 __device__ void select_top8(const bf16* __restrict__ logits, unsigned n_experts,
                             int (&ids)[kMoeTopK], float (&vals)[kMoeTopK]) {
   const int lane = threadIdx.x & 63;
+  // all four logits are requested before any is used (clamped index: one
+  // memory round trip, not one per branch)
+  unsigned short raw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned e = lane + 64 * i;
+    raw[i] = __builtin_bit_cast(unsigned short, logits[e < n_experts ? e : 0u]);
+  }
   unsigned key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const unsigned e = lane + 64 * i;
-    unsigned k = 0;
-    if (e < n_experts) {
-      const unsigned b = __builtin_bit_cast(unsigned short, logits[e]);
-      const unsigned ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-      k = (ord << 16) | (0xFFFFu - e);
-    }
-    key[i] = k;
+    const unsigned b = raw[i];
+    const unsigned ord = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+    key[i] = e < n_experts ? (ord << 16) | (0xFFFFu - e) : 0u;
   }
 #pragma unroll
   for (int r = 0; r < kMoeTopK; ++r) {
