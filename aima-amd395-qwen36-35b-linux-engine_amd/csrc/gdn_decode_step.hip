@@ -95,7 +95,12 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
   for (int e = 0; e < 4; ++e) nw[e] = bf2f(nw_raw[e]);
 
   const float qscale = 0.08838834764831845f;  // 1/sqrt(128)
-  for (unsigned t = 0; t < tokens; ++t) {
+  // tokens >= 1 (the entry point rejects 0): a do-while has no guard
+  // branch, so the compiler keeps every input load above in the first
+  // block instead of sinking them below the guard after the state loads'
+  // wait (a second memory round trip)
+  unsigned t = 0;
+  do {
     const int par = t & 1;
     const float cur = bf2f(x_raw);
     const float av = bf2f(a_raw), bv = bf2f(b_raw);
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(kDsThreads) void gdn_decode_step_kernel(
         *reinterpret_cast<bf16x4*>(out + (size_t)t * (kGdnHv * kGdnDv) + h * kGdnDv + 4 * cq) = res;
       }
     }
-  }
+  } while (++t < tokens);
 #pragma unroll
   for (int i = 0; i < kDsRowsPerThread; ++i)
     *reinterpret_cast<f32x4*>(state_out + sbase + (size_t)(r0 + i) * kGdnDv) = s[i];
