@@ -390,6 +390,12 @@ __global__ __launch_bounds__(64 * kFmWaves, 1) void fmha_prefill_kernel(
 // chunks' partials: M = max m_c, L = sum l_c 2^(m_c - M), O = sum O_c 2^(m_c -
 // M) / L (chunks where the row saw no key have l = 0 and weigh nothing).
 // grid = tiles x 16 heads x 16 row groups; block = 512 (16 rows x 32 dims/8).
+// Every (m, l) pair, the first four chunks' O partials and the gate are
+// requested together (indices clamped to the live range, so every load is
+// unconditional and in bounds): one memory round trip for up to four live
+// chunks, where per-chunk loads behind the l > 0 test cost two each.
+constexpr int kCombineMaxChunks = 16;   // split_plan: n_chunks <= 256 / 16
+template <int kMaxC>   // n_chunks <= kMaxC (4 or kCombineMaxChunks)
 __global__ __launch_bounds__(512) void fmha_split_combine_kernel(
     const float* __restrict__ po, const float* __restrict__ pml, float* __restrict__ out,
     unsigned q_tokens, unsigned kv_tokens, unsigned chunk_keys, unsigned n_chunks,
@@ -402,32 +408,55 @@ __global__ __launch_bounds__(512) void fmha_split_combine_kernel(
   const int d0 = 8 * (threadIdx.x & 31);
   const unsigned off = kv_tokens - q_tokens;
   const unsigned kv_end = min(kv_tokens, min(qtile * kRows + kRows, q_tokens) + off);
-  const unsigned live = (kv_end + chunk_keys - 1) / chunk_keys;
-  float M = -INFINITY;
-  for (unsigned c = 0; c < live; ++c) {
-    const size_t item = ((size_t)qtile * n_chunks + c) * kHq + head;
-    const float2 ml = *reinterpret_cast<const float2*>(pml + (item * kRows + r) * 2);
-    if (ml.y > 0.f) M = fmaxf(M, ml.x);
-  }
-  float L = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (unsigned c = 0; c < live; ++c) {
-    const size_t item = ((size_t)qtile * n_chunks + c) * kHq + head;
-    const float2 ml = *reinterpret_cast<const float2*>(pml + (item * kRows + r) * 2);
-    if (!(ml.y > 0.f)) continue;
-    const float w = __builtin_amdgcn_exp2f(ml.x - M);
-    L += w * ml.y;
-    const f32x4* src = reinterpret_cast<const f32x4*>(po + (item * kRows + r) * kD + d0);
-    const f32x4 a = src[0], b = src[1];
+  const unsigned live = (kv_end + chunk_keys - 1) / chunk_keys;   // 1 .. n_chunks
+  auto item_of = [&](unsigned c) {
+    return ((size_t)qtile * n_chunks + min(c, live - 1)) * kHq + head;
+  };
+  float2 ml[kMaxC];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[e] += w * a[e];
-      acc[4 + e] += w * b[e];
+  for (int c = 0; c < kMaxC; ++c)
+    ml[c] = *reinterpret_cast<const float2*>(pml + (item_of(c) * kRows + r) * 2);
+  f32x4 oa[4], ob[4];
+  auto load_o = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(po + (item_of(c0 + j) * kRows + r) * kD + d0);
+      oa[j] = src[0];
+      ob[j] = src[1];
+    }
+  };
+  load_o(0);
+  // gated: the gate row (any valid address otherwise; the value is unused)
+  const bf16* gp = ga.out != nullptr
+                       ? ga.gate + (size_t)row * ga.gate_stride + head * 2 * kD + kD + d0
+                       : reinterpret_cast<const bf16*>(po + (item_of(0) * kRows + r) * kD + d0);
+  const bf16x8 g = *reinterpret_cast<const bf16x8*>(gp);
+  __builtin_amdgcn_sched_barrier(0);
+  float M = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < kMaxC; ++c)
+    if ((unsigned)c < live && ml[c].y > 0.f) M = fmaxf(M, ml[c].x);
+  float L = 0.f, acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int c0 = 0; c0 < kMaxC; c0 += 4) {
+    if ((unsigned)c0 >= live) break;
+    if (c0 > 0) load_o(c0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float2 m_l = ml[c0 + j];
+      if ((unsigned)(c0 + j) < live && m_l.y > 0.f) {
+        const float w = __builtin_amdgcn_exp2f(m_l.x - M);
+        L += w * m_l.y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += w * oa[j][e];
+          acc[4 + e] += w * ob[j][e];
+        }
+      }
     }
   }
   const float inv = 1.0f / L;
   if (ga.out != nullptr) {   // gated bf16 rows (see GateArgs)
-    const bf16x8 g = *reinterpret_cast<const bf16x8*>(ga.gate + (size_t)row * ga.gate_stride +
-                                                      head * 2 * kD + kD + d0);
     const bf16x4 lo = gate4_bf16_fast(f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv},
                                       bf16x4{g[0], g[1], g[2], g[3]});
     const bf16x4 hi = gate4_bf16_fast(f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv},
@@ -493,6 +522,7 @@ SplitPlan split_plan(unsigned q_tokens, unsigned kv_tokens) {
   p.chunk_keys = (((kv_tokens + p.n_chunks - 1) / p.n_chunks) + kFmKv - 1) / kFmKv * kFmKv;
   p.items = tiles * p.n_chunks * kHq;
   if (p.n_chunks < 2 || p.items > kSplitItems) p = SplitPlan{1u, kv_tokens, 0u};
+  static_assert(256 / kHq <= kCombineMaxChunks, "the combine holds every chunk's (m, l)");
   return p;
 }
 
@@ -540,9 +570,10 @@ int launch_fmha(const void* q, const void* k, const void* v, float* out,
     sp.n_chunks = plan.n_chunks;
     hipLaunchKernelGGL((fmha_prefill_kernel<8, true>), dim3(plan.items), dim3(512), kFmLds,
                        stream, qb, kb, vb, out, q_tokens, kv_tokens, tiles(256), sp, ga);
-    hipLaunchKernelGGL(fmha_split_combine_kernel, dim3(tiles(256) * kHq * 16), dim3(512), 0,
-                       stream, sp.o, sp.ml, out, q_tokens, kv_tokens, plan.chunk_keys,
-                       plan.n_chunks, ga);
+    auto combine = plan.n_chunks <= 4 ? fmha_split_combine_kernel<4>
+                                      : fmha_split_combine_kernel<kCombineMaxChunks>;
+    hipLaunchKernelGGL(combine, dim3(tiles(256) * kHq * 16), dim3(512), 0, stream, sp.o, sp.ml,
+                       out, q_tokens, kv_tokens, plan.chunk_keys, plan.n_chunks, ga);
     return static_cast<int>(hipGetLastError());
   }
   if (ga.out != nullptr) {   // gated: 256-row workgroups at every length
