@@ -186,7 +186,12 @@ Q36_EXPORT int qwen36_head_norm_rope(
   const int st = ensure_inv_freq();
   if (st != Q36_OK) return st;
   const auto a8 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; };
-  if (a8(q_gate) && a8(k_raw) && a8(v_raw) && a8(q_out) && a8(k_cache) && a8(v_cache) &&
+  // One wave per token needs long prompts to fill the GPU; shorter ones run
+  // one wave per (token, head).  Graph-replayed on MI355X, rows form vs
+  // per-head form: T = 512 10.4 vs 5.2 us, 1024 11.3 vs 7.9, 2048 14.1 vs
+  // 12.5, 4096 21.1 vs 22.0, 8192 33.1 vs 41.4 (bit-identical forms).
+  constexpr unsigned kRowsFormMinTokens = 3072;
+  if (tokens >= kRowsFormMinTokens && a8(q_gate) && a8(k_raw) && a8(v_raw) && a8(q_out) && a8(k_cache) && a8(v_cache) &&
       (q_row_stride % 4) == 0 && (k_row_stride % 4) == 0 && (v_row_stride % 4) == 0) {
     hipLaunchKernelGGL(head_norm_rope_rows_kernel, dim3((tokens + 3) / 4), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const bf16*>(q_gate),

@@ -314,12 +314,12 @@ def test_gated_prefill_every_gate_value(gpu, t):
     assert nan.sum().item() == 254 * t * 4096 // 65536   # the NaN patterns only
 
 
-@pytest.mark.parametrize("t,pos", [(1, 0), (5, 4093), (300, 0), (1000, 123457)])
+@pytest.mark.parametrize("t,pos", [(3072, 0), (3077, 4093), (4100, 123457)])
 def test_head_norm_rope_rows_kernel_matches_per_head_form(gpu, t, pos):
-    """The one-wave-per-token head norm + RoPE kernel (8-byte aligned rows)
-    gives the per-(token, head) kernel's bits (the same rows through an
-    odd-strided view, which the library routes to that form): q, the
-    normalised K rows and the raw V rows in the caches."""
+    """The one-wave-per-token head norm + RoPE kernel (8-byte aligned rows,
+    from 3072 tokens) gives the per-(token, head) kernel's bits (the same
+    rows through an odd-strided view, which the library routes to that
+    form): q, the normalised K rows and the raw V rows in the caches."""
     from qwen36_attn.full_attention import head_norm_rope_kv_write
     from qwen36_attn import synthetic as syn
     g = syn.gen(60 + t)
