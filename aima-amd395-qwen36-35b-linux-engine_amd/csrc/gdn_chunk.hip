@@ -421,12 +421,16 @@ constexpr int kScanGroups = kGdnDv / 16;   // 16 v-columns per workgroup
 // (row-major, pitch kPitchR: conflict-free 16-byte row writes and
 // fragment reads; k^T operands come from the same rows through transposed
 // reads) and the record's scalars.
+typedef bf16x4 XBlk[2][2][2][64];
+
 struct ScanLds {
   bf16x8 st[4][2][64];        // [state tile pair][hi, lo][lane]: B operands
-  // Exchanged token tiles as ready B operands: [32-token block][hi, lo]
-  // [lane]; token tile t fills elements 4 (t % 2) .. +3 of block t / 2.
-  bf16x8 z[2][2][64];         // v - cy (k S)
-  bf16x8 vp[2][2][2][64];     // [v', rsk v'][block][hi, lo][lane]
+  // Exchanged token tiles: [32-token block][hi, lo][tile parity][lane];
+  // token tile t holds elements 4 (t % 2) .. +3 of its block's B operand,
+  // so a reader joins the two parities (one ds_read2_b64) and every writer
+  // lane stores 8 contiguous bytes.
+  XBlk z;                     // v - cy (k S)
+  XBlk vp[2];                 // v', rsk v'
   bf16 qr[2][kC * kPitchR];
   bf16 kr[2][kC * kPitchR];
   float sc[2][kNsc * 64];
@@ -460,12 +464,17 @@ __device__ __forceinline__ bf16x8 split4(const f32x4& x) {
 }
 
 // Publish token tile t of an exchanged pair of B operands (see ScanLds).
-__device__ __forceinline__ void put_tile(bf16x8 (&blk)[2][2][64], int t, int lane,
-                                         const f32x4& x) {
+__device__ __forceinline__ void put_tile(XBlk& blk, int t, int lane, const f32x4& x) {
   bf16x4 hi, lo;
   split4x(x, hi, lo);
-  *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(&blk[t >> 1][0][lane]) + 4 * (t & 1)) = hi;
-  *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(&blk[t >> 1][1][lane]) + 4 * (t & 1)) = lo;
+  blk[t >> 1][0][t & 1][lane] = hi;
+  blk[t >> 1][1][t & 1][lane] = lo;
+}
+
+// The B operand of 32-token block b, plane pl (0 = hi, 1 = lo).
+__device__ __forceinline__ bf16x8 get_blk(const XBlk& blk, int b, int pl, int lane) {
+  const bf16x4 a = blk[b][pl][0][lane], c = blk[b][pl][1][lane];
+  return bf16x8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
 }
 
 // B operands (hi, lo) from two published accumulator tiles.
@@ -647,7 +656,7 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         if (t2 == 1 && w < 2) break;
-        const bf16x8 vh = s.vp[0][t2][0][lane], vl = s.vp[0][t2][1][lane];
+        const bf16x8 vh = get_blk(s.vp[0], t2, 0, lane), vl = get_blk(s.vp[0], t2, 1, lane);
         acc = mfma16x16x32(ah[t2], vh, acc);
         acc2 = mfma16x16x32(ah[t2], vl, acc2);
         acc3 = mfma16x16x32(al[t2], vh, acc3);
@@ -752,7 +761,7 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
 #pragma unroll
       for (int t2 = 0; t2 < 2; ++t2) {
         if (t2 == 1 && w < 2) break;
-        const bf16x8 zh = s.z[t2][0][lane], zl = s.z[t2][1][lane];
+        const bf16x8 zh = get_blk(s.z, t2, 0, lane), zl = get_blk(s.z, t2, 1, lane);
         vp = mfma16x16x32(th[t2], zh, vp);
         vp2 = mfma16x16x32(th[t2], zl, vp2);
         vp3 = mfma16x16x32(tl[t2], zh, vp3);
@@ -769,7 +778,7 @@ __global__ __launch_bounds__(768, 1) void gdn_chunk_scan_kernel(
     f32x4 sl[2] = {zero, zero};
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      const bf16x8 zh = s.vp[1][t2][0][lane], zl = s.vp[1][t2][1][lane];
+      const bf16x8 zh = get_blk(s.vp[1], t2, 0, lane), zl = get_blk(s.vp[1], t2, 1, lane);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         // k^T A operand (row = dim 16(2w+i) + li, reduction = tokens
