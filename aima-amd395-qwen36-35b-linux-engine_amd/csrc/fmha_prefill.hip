@@ -509,17 +509,31 @@ std::once_flag g_fm_attr_once;
 hipError_t g_fm_attr_status = hipSuccess;
 
 // Split plan for short prompts: too few 256-row tiles to fill the GPU, so
-// each tile's key range is cut into chunks (about 256 live workgroups).
+// each tile's key range is cut into n chunks (a multiple of 32 keys; a
+// tile's chunks past its last key exit at once).  The chunk count was
+// swept on MI355X (n = 2 .. 16 and unsplit, graph-replayed):
+//  * square prompts (no cached prefix): the best n by 256-row tile count,
+//    kSquareChunks below (T = 256: 23.9 us at n = 2 against 27.7 at 16;
+//    T = 2304 / 2560: 85 / 97 us at n = 3 against 92 / 107 at 2);
+//  * rows over a prefix: about 256 workgroups (n = 256 / (16 tiles));
+//  * from 11 tiles on (T > 2560) the unsplit kernel is faster than any
+//    split that fits the scratch (T = 3072 128 vs 137 us, T = 3840 165 vs
+//    182; 3072 rows over a 4096 prefix 290 vs 327).
 struct SplitPlan {
   unsigned n_chunks, chunk_keys, items;
 };
 
+constexpr unsigned kSplitMaxTiles = 10;
+constexpr unsigned char kSquareChunks[kSplitMaxTiles + 1] = {0, 2, 8, 6, 4, 4, 3, 3, 2, 3, 3};
+
 SplitPlan split_plan(unsigned q_tokens, unsigned kv_tokens) {
   const unsigned tiles = (q_tokens + 255) / 256;
   SplitPlan p{1u, kv_tokens, 0u};
-  if (tiles * kHq >= 256u) return p;
-  p.n_chunks = (256u + tiles * kHq - 1) / (tiles * kHq);
+  if (tiles > kSplitMaxTiles) return p;
+  p.n_chunks = kv_tokens - q_tokens < 256u ? kSquareChunks[tiles]
+                                           : (256u + tiles * kHq - 1) / (tiles * kHq);
   p.chunk_keys = (((kv_tokens + p.n_chunks - 1) / p.n_chunks) + kFmKv - 1) / kFmKv * kFmKv;
+  p.n_chunks = (kv_tokens + p.chunk_keys - 1) / p.chunk_keys;   // after rounding up
   p.items = tiles * p.n_chunks * kHq;
   if (p.n_chunks < 2 || p.items > kSplitItems) p = SplitPlan{1u, kv_tokens, 0u};
   static_assert(256 / kHq <= kCombineMaxChunks, "the combine holds every chunk's (m, l)");
