@@ -68,16 +68,25 @@ __global__ __launch_bounds__(256) void gdn_conv1d_kernel(
 
 // Vector form of gdn_conv1d_kernel (16-byte loads and stores, the same
 // conv arithmetic; SiLU through silu_fast with the exact form where it could
-// differ, so the same bits for every finite input): grid = (C/2048, ceil(T/8));
-// thread = 8 consecutive channels, 8 consecutive tokens, whose input rows
-// are all requested before the first output is formed (T = 8192 on MI355X:
-// 8 tokens per thread 54 us, 16: 63 us, 4: 66 us, 32: 76 us).
+// differ, so the same bits for every finite input): grid = (C/2048,
+// ceil(T/TPT)); thread = 8 consecutive channels, TPT consecutive tokens.
+// Two load orders (MI355X, graph-replayed):
+//  * kUpfront: every row and the state requested unconditionally before
+//    the first use (the first block's three history rows read row 0 and
+//    are replaced by the state at use) -- one memory round trip, for short
+//    prompts, where few waves are resident (TPT = 4: T = 512 7.3 us,
+//    1024 11.6, 2048 18.4, 4096 30.8);
+//  * otherwise each row behind its own (tok >= 0) test, which costs a round
+//    trip per row but keeps fewer registers live -- at T = 8192 the
+//    occupancy hides the latency (TPT = 8: 54 us; 16: 63, 4: 66, 32: 76;
+//    the up-front form there: 57.6-59.6 us).
+template <int TPT, bool kUpfront>
 __global__ __launch_bounds__(256) void gdn_conv1d_vec_kernel(
     const bf16* __restrict__ x, unsigned x_row_stride,
     const bf16* __restrict__ weight, const bf16* __restrict__ state_in,
     bf16* __restrict__ state_out, bf16* __restrict__ out, unsigned tokens) {
   const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-  const unsigned t0 = blockIdx.y * kConvTokensPerThread;
+  const unsigned t0 = blockIdx.y * TPT;
   float w[8][kGdnConvK];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -86,32 +95,56 @@ __global__ __launch_bounds__(256) void gdn_conv1d_vec_kernel(
     for (int e = 0; e < 8; ++e) w[2 * i + e / 4][e % 4] = bf2f(wv[e]);
   }
   // window rows t0-3 .. t0-1 (from the state before the first token), then
-  // the thread's 8 rows (rows past the end re-read the last row, not stored)
-  bf16x8 rows[3 + kConvTokensPerThread];
+  // the thread's TPT rows (rows past the end re-read the last row, not stored)
+  bf16x8 rows[3 + TPT];
   bf16 st[24] = {};
-  if (blockIdx.y == 0) {   // only the first token block reads the state
+  if constexpr (kUpfront) {
     const bf16x8* sp = reinterpret_cast<const bf16x8*>(state_in + c0 * 3);
     const bf16x8 a = sp[0], b = sp[1], c = sp[2];
+#pragma unroll
+    for (int j = 0; j < 3 + TPT; ++j) {
+      const int tok = (int)t0 - 3 + j;
+      const unsigned tc = min((unsigned)max(tok, 0), tokens - 1);
+      rows[j] = *reinterpret_cast<const bf16x8*>(x + (size_t)tc * x_row_stride + c0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       st[e] = a[e];
       st[8 + e] = b[e];
       st[16 + e] = c[e];
     }
-  }
+  } else {
+    if (blockIdx.y == 0) {   // only the first token block reads the state
+      const bf16x8* sp = reinterpret_cast<const bf16x8*>(state_in + c0 * 3);
+      const bf16x8 a = sp[0], b = sp[1], c = sp[2];
 #pragma unroll
-  for (int j = 0; j < 3 + kConvTokensPerThread; ++j) {
-    const int tok = (int)t0 - 3 + j;
-    if (tok >= 0) {
-      const unsigned tc = min((unsigned)tok, tokens - 1);
-      rows[j] = *reinterpret_cast<const bf16x8*>(x + (size_t)tc * x_row_stride + c0);
-    } else {
+      for (int e = 0; e < 8; ++e) {
+        st[e] = a[e];
+        st[8 + e] = b[e];
+        st[16 + e] = c[e];
+      }
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) rows[j][e] = st[e * 3 + (tok + 3)];
+    for (int j = 0; j < 3 + TPT; ++j) {
+      const int tok = (int)t0 - 3 + j;
+      if (tok >= 0) {
+        const unsigned tc = min((unsigned)tok, tokens - 1);
+        rows[j] = *reinterpret_cast<const bf16x8*>(x + (size_t)tc * x_row_stride + c0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) rows[j][e] = st[e * 3 + (tok + 3)];
+      }
     }
   }
+  // row j's value of channel e (up-front: the first block's history rows
+  // come from the state)
+  const bool from_state = kUpfront && blockIdx.y == 0;
+  auto val = [&](int j, int e) {
+    return (j < 3 && from_state) ? bf2f(st[e * 3 + j]) : bf2f(rows[j][e]);
+  };
 #pragma unroll
-  for (int j = 0; j < kConvTokensPerThread; ++j) {
+  for (int j = 0; j < TPT; ++j) {
     const unsigned t = t0 + j;
     // SiLU from the hardware exp2 / rcp; the exact form only where the fast
     // value could round to another bf16 (one branch per row of 8)
@@ -119,10 +152,10 @@ __global__ __launch_bounds__(256) void gdn_conv1d_vec_kernel(
     bool slow = false;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float acc = mul_rn(bf2f(rows[j][e]), w[e][0]);
-      acc = add_rn(acc, mul_rn(bf2f(rows[j + 1][e]), w[e][1]));
-      acc = add_rn(acc, mul_rn(bf2f(rows[j + 2][e]), w[e][2]));
-      acc = add_rn(acc, mul_rn(bf2f(rows[j + 3][e]), w[e][3]));
+      float acc = mul_rn(val(j, e), w[e][0]);
+      acc = add_rn(acc, mul_rn(val(j + 1, e), w[e][1]));
+      acc = add_rn(acc, mul_rn(val(j + 2, e), w[e][2]));
+      acc = add_rn(acc, mul_rn(val(j + 3, e), w[e][3]));
       cv[e] = bf2f(f2bf(acc));
       bool sl;
       sv[e] = silu_fast(cv[e], sl);
@@ -275,7 +308,11 @@ Q36_EXPORT int qwen36_gdn_conv1d(const void* x, unsigned x_row_stride,
   const bool vec = aligned16(x) && aligned16(weight) && aligned16(state_in) &&
                    aligned16(state_out) && aligned16(out) && (x_row_stride % 8) == 0;
   if (vec) {
-    hipLaunchKernelGGL(gdn_conv1d_vec_kernel, dim3(kGdnConvDim / 2048, tblocks), dim3(256), 0,
+    // short prompts: 4 tokens per thread, every load up front (see the kernel)
+    const bool short_form = tokens <= 4096u;
+    const unsigned tpt = short_form ? 4u : 8u;
+    auto kernel = short_form ? gdn_conv1d_vec_kernel<4, true> : gdn_conv1d_vec_kernel<8, false>;
+    hipLaunchKernelGGL(kernel, dim3(kGdnConvDim / 2048, (tokens + tpt - 1) / tpt), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const bf16*>(x),
                        x_row_stride, static_cast<const bf16*>(weight),
                        static_cast<const bf16*>(state_in), static_cast<bf16*>(state_out),
