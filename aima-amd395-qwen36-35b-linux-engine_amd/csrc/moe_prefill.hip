@@ -89,7 +89,7 @@ enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
 // three regions (expert ids, routing weights, router logits) are read back by
 // the host's debug path at these fixed offsets.
 struct PfLayout {
-  size_t ids, rw, logits, sgw, meta, sorted, hist, after, h2, act, y, total;
+  size_t ids, rw, logits, sgw, meta, sorted, hist, after, h2, act, y, act_shared, total;
   unsigned ld_logits, max_tiles, max_rows, n_chunks, chunk_ids;
 };
 
@@ -115,6 +115,7 @@ PfLayout pf_layout(unsigned T, unsigned E) {
   L.h2 = o;      o = align256(o + (size_t)T * kMoeHidden * 2);
   L.act = o;     o = align256(o + (size_t)L.max_rows * kMoeInter * 2);
   L.y = o;       o = align256(o + (size_t)9 * T * kMoeHidden * 2);
+  L.act_shared = o;  o = align256(o + (size_t)T * kMoeInter * 2);
   L.total = o;
   return L;
 }
@@ -182,8 +183,8 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
 }
 
 // ---- 4. slots sorted by group, groups padded to 32 rows, 128-row tiles ----
-// sorted[p] = slot (t * 8 + k for routed rank k of token t, 8T + t for the
-// shared expert) or -1 for padding; group g occupies rows [row_off[g],
+// sorted[p] = slot (t * 8 + k for routed rank k of token t) or -1 for
+// padding (the shared expert, every token, runs as launches of its own); group g occupies rows [row_off[g],
 // row_off[g] + roundup32(n_g)).  meta (int4) [0] = {tiles}, [1 + i] =
 // {group, first row, rows, 0} for tile i.  The 8T ids are cut into chunks of
 // kAlignChunk: hist[g][chunk] counts, the scan turns them into each chunk's
@@ -243,7 +244,7 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, 
     sum += __shfl_xor(sum, 1, 64);
     sum += __shfl_xor(sum, 2, 64);
     if (g < E && part == 0) cnt[g] = sum;
-    if (tid == 0) cnt[E] = (int)T;
+    if (tid == 0) cnt[E] = 0;   // the shared expert runs as launches of its own
   }
   __syncthreads();
   if (tid < 64) {   // one wave: exclusive scans of padded rows and tiles per group
@@ -325,8 +326,6 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, 
       }
     }
   }
-  const int shared0 = row_off[E];
-  for (unsigned t = tid; t < T; t += blockDim.x) sorted[shared0 + t] = (int)(routed + t);
 }
 
 // 4c. per-chunk scatter: slot i goes to its group's next row of this chunk.
@@ -372,6 +371,7 @@ struct GemmArgs {
   const float* sgw;
   bf16* out;                // logits / act / y
   unsigned T, E, ld_out, max_items;
+  unsigned shared;          // gate/up, down: the shared expert's T rows in token order
 };
 
 // The leading s_nop covers a hazard the compiler cannot see through the
@@ -449,7 +449,8 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
   constexpr int K = MODE == kDown ? kMoeInter : kMoeHidden;
   constexpr int nsteps = K / kPfBK;
   const unsigned nb = n_blocks<MODE>(p.E);
-  const unsigned m_tiles = MODE == kRouter ? (p.T + kPfBM - 1) / kPfBM : (unsigned)p.meta[0].x;
+  const unsigned m_tiles = (MODE == kRouter || p.shared) ? (p.T + kPfBM - 1) / kPfBM
+                                                          : (unsigned)p.meta[0].x;
   const unsigned items = m_tiles * nb;
   const unsigned share = (items + 7) / 8;
   const unsigned xi = blockIdx.x >> 3;
@@ -458,7 +459,8 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
   if (item >= items) return;
   const unsigned mt = item / nb, nt = item % nb;
   int group = 0, row0, rows;
-  if constexpr (MODE == kRouter) {
+  if (MODE == kRouter || p.shared) {
+    group = MODE == kRouter ? 0 : (int)p.E;
     row0 = (int)(mt * kPfBM);
     rows = min(kPfBM, (int)p.T - row0);
   } else {
@@ -507,7 +509,8 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
       if constexpr (MODE == kRouter) {
         off = r < rows ? (unsigned)(row0 + r) * kMoeHidden * 2u : kOob;
       } else if constexpr (MODE == kGateUp) {
-        const int slot = r < rows ? p.sorted[row0 + r] : -1;
+        const int slot = r >= rows ? -1
+                         : p.shared ? (int)(kMoeTopK * p.T) + row0 + r : p.sorted[row0 + r];
         const unsigned routed = kMoeTopK * p.T;
         const unsigned t = slot < 0 ? 0u : ((unsigned)slot < routed ? (unsigned)slot / kMoeTopK
                                                                     : (unsigned)slot - routed);
@@ -598,9 +601,15 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
         const unsigned c = nt * (kPfBN / 2) + 32 * wn + li;
         const float g = bf2f(f2bf(acc[rb][0][i])), u = bf2f(f2bf(acc[rb][1][i]));
         p.out[(size_t)(row0 + r) * kMoeInter + c] = f2bf(silu_f(g) * u);
+      } else if (p.shared) {
+        // the shared expert's row, unscaled: the combine applies the shared
+        // gate (known only after the router) with this epilogue's roundings
+        bf16* y = p.out + (size_t)(routed + row0 + r) * kMoeHidden + nt * kPfBN + 64 * wn + li;
+        y[0] = f2bf(acc[rb][0][i]);
+        y[32] = f2bf(acc[rb][1][i]);
       } else {
         const int slot = p.sorted[row0 + r];
-        const float w = (unsigned)slot < routed ? p.rw[slot] : p.sgw[slot - routed];
+        const float w = p.rw[slot];
         bf16* y = p.out + (size_t)slot * kMoeHidden + nt * kPfBN + 64 * wn + li;
         y[0] = f2bf(bf2f(f2bf(acc[rb][0][i])) * w);
         y[32] = f2bf(bf2f(f2bf(acc[rb][1][i])) * w);
@@ -613,8 +622,8 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
 // moe = bf16(sum over ranks 0..7 of y, fp32 in rank order); out = bf16(after +
 // bf16(moe + shared)) -- the order of qwen36_moe_decode's combine.
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const bf16* __restrict__ y, const bf16* __restrict__ after, bf16* __restrict__ out,
-    unsigned T) {
+    const bf16* __restrict__ y, const bf16* __restrict__ after, const float* __restrict__ sgw,
+    bf16* __restrict__ out, unsigned T) {
   const unsigned t = blockIdx.x;
   const int c = 8 * threadIdx.x;
   float moe[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -625,6 +634,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   const bf16x8 ys = *reinterpret_cast<const bf16x8*>(
       y + ((size_t)kMoeTopK * T + t) * kMoeHidden + c);
   const bf16x8 af = *reinterpret_cast<const bf16x8*>(after + (size_t)t * kMoeHidden + c);
+  const float sg = sgw[t];
 #pragma unroll
   for (int k = 0; k < kMoeTopK; ++k)
 #pragma unroll
@@ -632,11 +642,29 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   bf16x8 o;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float total = bf2f(f2bf(bf2f(f2bf(moe[e])) + bf2f(ys[e])));
+    const float shared = bf2f(f2bf(bf2f(ys[e]) * sg));   // the shared row scaled by its gate
+    const float total = bf2f(f2bf(bf2f(f2bf(moe[e])) + shared));
     o[e] = f2bf(bf2f(af[e]) + total);
   }
   *reinterpret_cast<bf16x8*>(out + (size_t)t * kMoeHidden + c) = o;
 }
+
+// The shared expert depends only on the normalised rows (its gate is applied
+// in the combine), so its two GEMMs run on a side stream while the router,
+// top-8 and alignment chain -- a few latency-bound launches that leave most
+// CUs idle -- runs on the caller's stream, and the routed GEMMs then hold
+// only the routed tiles.  One side stream and a fork / join event pair per
+// device, created on first use; the mutex keeps each call's record / wait
+// pairs together when several host threads enqueue at once.  If they cannot
+// be created, everything runs on the caller's stream.
+constexpr int kPfMaxDevices = 64;
+struct SideStream {
+  bool tried = false;
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mutex;
+SideStream g_side[kPfMaxDevices];
 
 }  // namespace
 }  // namespace q36
@@ -702,6 +730,21 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned tok_blocks = (T + 3) / 4;
 
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kPfMaxDevices) return Q36_EINVAL;
+  std::lock_guard<std::mutex> lock(g_side_mutex);
+  SideStream& side = g_side[dev];
+  if (!side.tried) {
+    side.tried = true;
+    if (hipStreamCreateWithFlags(&side.s, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&side.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&side.join, hipEventDisableTiming) != hipSuccess) {
+      (void)hipGetLastError();
+      side.s = nullptr;
+    }
+  }
+  hipStream_t ss = side.s != nullptr ? side.s : st;
+
   hipLaunchKernelGGL(moe_pre_kernel, dim3(tok_blocks), dim3(256), 0, st,
                      static_cast<const bf16*>(inp), static_cast<const bf16*>(attn_out),
                      static_cast<const bf16*>(post_norm_w), after, h2, T);
@@ -714,6 +757,30 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   g.rw = rw;
   g.sgw = sgw;
   auto grid_for = [](unsigned max_items) { return dim3(8 * ((max_items + 7) / 8)); };
+
+  // shared expert: gate/up then down (unscaled rows into its y slots) on
+  // the side stream
+  if (ss != st) {
+    if (hipEventRecord(side.fork, st) != hipSuccess || hipStreamWaitEvent(ss, side.fork, 0) != hipSuccess)
+      return static_cast<int>(hipGetLastError());
+  }
+  bf16* act_shared = reinterpret_cast<bf16*>(ws + L.act_shared);
+  const unsigned shared_items = (T + kPfBM - 1) / kPfBM;
+  GemmArgs gs = g;
+  gs.shared = 1;
+  gs.a = h2;
+  gs.w = static_cast<const bf16*>(expert_gate_up);
+  gs.w_shared = win + (size_t)(E + 1) * kMoeHidden;
+  gs.out = act_shared;
+  gs.max_items = shared_items * n_blocks<kGateUp>(E);
+  hipLaunchKernelGGL(moe_gemm_kernel<kGateUp>, grid_for(gs.max_items), dim3(64 * kPfWaves), kPfLds, ss, gs);
+  gs.a = act_shared;
+  gs.w = static_cast<const bf16*>(expert_down);
+  gs.w_shared = static_cast<const bf16*>(shared_down);
+  gs.out = y;
+  gs.max_items = shared_items * n_blocks<kDown>(E);
+  hipLaunchKernelGGL(moe_gemm_kernel<kDown>, grid_for(gs.max_items), dim3(64 * kPfWaves), kPfLds, ss, gs);
+  if (ss != st && hipEventRecord(side.join, ss) != hipSuccess) return static_cast<int>(hipGetLastError());
 
   g.a = h2;
   g.w = win;
@@ -747,7 +814,9 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   g.max_items = L.max_tiles * n_blocks<kDown>(E);
   hipLaunchKernelGGL(moe_gemm_kernel<kDown>, grid_for(g.max_items), dim3(64 * kPfWaves), kPfLds, st, g);
 
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, st, y, after,
+  if (ss != st && hipStreamWaitEvent(st, side.join, 0) != hipSuccess)
+    return static_cast<int>(hipGetLastError());
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, st, y, after, sgw,
                      static_cast<bf16*>(out), T);
   return static_cast<int>(hipGetLastError());
 }

@@ -161,6 +161,32 @@ def test_graph_gdn_decode_step_and_moe_decode(gpu):
     _replay_and_check(graph, lambda: None, [gout, new_conv, fin, mout], refs, between)
 
 
+def test_graph_moe_prefill_with_side_stream(gpu):
+    """The MoE block over T tokens: its shared-expert GEMMs run on the
+    library's side stream between a fork and a join event recorded on the
+    caller's stream, so the capture takes them into the graph as a branch."""
+    from qwen36_attn.moe import MoEBlock
+    g = syn.gen(904)
+    w = {k_: v_.to(gpu) for k_, v_ in syn.moe_weights(g, n_experts=64).items()}
+    block = MoEBlock(w)
+    inp = syn.randn((300, 2048), g, 0.5).to(gpu)
+    attn = syn.randn((300, 2048), g, 0.5).to(gpu)
+    out = torch.empty(300, 2048, dtype=torch.bfloat16, device=gpu)
+    print("graph: moe prefill T=300 (64 experts, side stream)", flush=True)
+
+    def run():
+        block.prefill(inp, attn, out=out)
+
+    run()
+    torch.cuda.synchronize()
+    refs = [out.clone()]
+    graph = _capture(run)
+
+    def between(i):
+        block.prefill(attn[:100], inp[:100])
+    _replay_and_check(graph, lambda: None, [out], refs, between)
+
+
 def test_scratch_refuses_to_grow_during_capture(gpu):
     """A call whose workspace would outgrow the shared scratch inside a
     capture raises instead of allocating graph-private memory."""
