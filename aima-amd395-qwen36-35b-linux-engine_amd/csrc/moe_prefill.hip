@@ -184,11 +184,12 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
 
 // ---- 4. slots sorted by group, groups padded to 32 rows, 128-row tiles ----
 // sorted[p] = slot (t * 8 + k for routed rank k of token t) or -1 for
-// padding (the shared expert, every token, runs as launches of its own); group g occupies rows [row_off[g],
-// row_off[g] + roundup32(n_g)).  meta (int4) [0] = {tiles}, [1 + i] =
-// {group, first row, rows, 0} for tile i.  The 8T ids are cut into chunks of
-// kAlignChunk: hist[g][chunk] counts, the scan turns them into each chunk's
-// first row per group, the scatter places the chunk's slots.  Order inside a
+// padding (the shared expert, every token, runs as launches of its own);
+// group g occupies rows [row_off[g], row_off[g] + roundup32(n_g)).  meta
+// (int4) [0] = {tiles}, [1 + i] = {group, first row, rows, 0} for tile i.
+// The 8T ids are cut into chunks of kAlignChunk: hist[g][chunk] counts, the
+// scan turns them into each chunk's first row per group, the scatter places
+// the chunk's slots.  Order inside a
 // group is arbitrary: every GEMM row is computed independently, so it does
 // not affect any value.
 
@@ -234,7 +235,7 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, 
   __shared__ int cnt[kMoeMaxExperts + 1];
   __shared__ int row_off[kMoeMaxExperts + 2];
   __shared__ int tile_off[kMoeMaxExperts + 2];
-  const unsigned G = E + 1, tid = threadIdx.x, routed = kMoeTopK * T;
+  const unsigned G = E + 1, tid = threadIdx.x;
   // totals: 4 threads per group, each summing a quarter of the chunks
   {
     const unsigned g = tid >> 2, part = tid & 3;
