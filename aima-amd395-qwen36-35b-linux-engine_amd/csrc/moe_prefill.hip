@@ -228,7 +228,7 @@ __global__ __launch_bounds__(256) void moe_hist_kernel(const int* __restrict__ i
 // 4b. one workgroup: group totals, row / tile offsets (one-wave scans), tile
 // table, padding, shared-expert rows, and hist turned into each chunk's
 // first row per group.
-__global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned T, unsigned E, unsigned n_chunks,
+__global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned E, unsigned n_chunks,
                                                         int* __restrict__ hist,
                                                         int4* __restrict__ meta,
                                                         int* __restrict__ sorted) {
@@ -796,7 +796,7 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   int* hist = reinterpret_cast<int*>(ws + L.hist);
   hipLaunchKernelGGL(moe_hist_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E, L.n_chunks,
                      L.chunk_ids, hist);
-  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, T, E, L.n_chunks, hist, meta,
+  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, E, L.n_chunks, hist, meta,
                      sorted);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E,
                      L.n_chunks, L.chunk_ids, hist, sorted);
