@@ -52,6 +52,31 @@ def test_prefill_config3_sampled_rows(gpu):
     assert torch.isfinite(got).all()
 
 
+@pytest.mark.parametrize("t", [256, 1536, 2304, 2560])
+def test_short_prompt_split_plans_sampled_rows(gpu, t):
+    """Short square prompts through the split plans the chunk-count table
+    picks (T = 256: 2 chunks, 1536: 3, 2304 and 2560: 3 over 9 and 10 query
+    tiles), plain and gated: rows at chunk and tile edges against the oracle."""
+    from qwen36_attn.full_attention import fmha_prefill, fmha_prefill_gated, output_gate
+    q, k, v = _inputs(t, t, seed=70 + t)
+    g = torch.Generator().manual_seed(71 + t)
+    gate = torch.randn(t, 8192, generator=g).to(torch.bfloat16)
+    print(f"short-prompt split plan T={t}", flush=True)
+    qd, kd, vd, gd = q.to(gpu), k.to(gpu), v.to(gpu), gate.to(gpu)
+    got = fmha_prefill(qd, kd, vd).cpu()
+    gated = fmha_prefill_gated(qd, kd, vd, gd).cpu()
+    rows = sorted({0, 1, 127, 128, 255, t // 3, t // 2 - 1, t // 2, 2 * t // 3, t - 257, t - 256,
+                   t - 2, t - 1} - {-1})
+    for r in rows:
+        ref = O.prefill_attention(q[r:r + 1], k[:r + 1], v[:r + 1], position_start=r,
+                                  out_dtype=torch.float32)
+        assert (got[r:r + 1] - ref).abs().max().item() <= TOL_TIGHT, r
+        gref = O.output_gate(ref.to(torch.bfloat16), O.split_q_gate(gate[r:r + 1])[1])
+        assert (gated[r:r + 1].float() - gref.float()).abs().max().item() <= TOL, r
+    assert torch.isfinite(got).all()
+    assert torch.equal(gated, output_gate(got.to(gpu), gd).cpu())
+
+
 def test_prefill_8k_causal_sampled_rows(gpu):
     """The benchmarked 8192-token causal prefill: rows spread over the whole
     range (tile and workgroup edges) against the oracle for those rows."""
