@@ -126,11 +126,12 @@ def test_config4_prefill_then_decode(gpu):
     assert rel_err(st.cpu(), ref_s2) <= TOL_STATE
 
 
-@pytest.mark.parametrize("t", [1, 2, 3, 17, 300, 1000])
+@pytest.mark.parametrize("t", [1, 2, 3, 17, 300, 1000, 4096, 4100])
 def test_vector_pointwise_kernels_match_scalar_forms(gpu, t):
     """The 16-byte conv and gated-norm kernels (aligned inputs) give the
     scalar kernels' bits (the same inputs through an odd-strided view, which
-    the library routes to the scalar forms)."""
+    the library routes to the scalar forms); the conv's short-prompt form
+    runs up to 4096 tokens, its long form from 4097."""
     from qwen36_attn import gated_deltanet as G
     g = syn.gen(40 + t)
     x = syn.randn((t, 8192), g)
