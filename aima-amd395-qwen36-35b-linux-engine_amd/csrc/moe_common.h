@@ -39,17 +39,9 @@ __device__ __forceinline__ unsigned wave_max_u32(unsigned v) {
 // flipped; else sign bit set), packed above 0xFFFF - expert so one unsigned
 // max picks the largest logit and, among equal ones, the lowest expert.
 // Lane l holds experts l + 64i.  (-0 ranks below +0; NaN logits unsupported.)
-__device__ void select_top8(const bf16* __restrict__ logits, unsigned n_experts,
-                            int (&ids)[kMoeTopK], float (&vals)[kMoeTopK]) {
+__device__ void select_top8_bits(const unsigned short (&raw)[4], unsigned n_experts,
+                                 int (&ids)[kMoeTopK], float (&vals)[kMoeTopK]) {
   const int lane = threadIdx.x & 63;
-  // all four logits are requested before any is used (clamped index: one
-  // memory round trip, not one per branch)
-  unsigned short raw[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const unsigned e = lane + 64 * i;
-    raw[i] = __builtin_bit_cast(unsigned short, logits[e < n_experts ? e : 0u]);
-  }
   unsigned key[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -71,6 +63,21 @@ __device__ void select_top8(const bf16* __restrict__ logits, unsigned n_experts,
     for (int i = 0; i < 4; ++i)
       if (key[i] == best) key[i] = 0u;
   }
+}
+
+// select_top8_bits over logits[0, n_experts) read from memory.
+__device__ void select_top8(const bf16* __restrict__ logits, unsigned n_experts,
+                            int (&ids)[kMoeTopK], float (&vals)[kMoeTopK]) {
+  const int lane = threadIdx.x & 63;
+  // all four logits are requested before any is used (clamped index: one
+  // memory round trip, not one per branch)
+  unsigned short raw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned e = lane + 64 * i;
+    raw[i] = __builtin_bit_cast(unsigned short, logits[e < n_experts ? e : 0u]);
+  }
+  select_top8_bits(raw, n_experts, ids, vals);
 }
 
 // Routing weights of the reference router (four_layer_mini_engine.py:7775-7789:

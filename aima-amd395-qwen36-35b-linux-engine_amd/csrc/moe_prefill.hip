@@ -89,9 +89,17 @@ enum GemmMode { kRouter = 0, kGateUp = 1, kDown = 2 };
 // three regions (expert ids, routing weights, router logits) are read back by
 // the host's debug path at these fixed offsets.
 struct PfLayout {
-  size_t ids, rw, logits, sgw, meta, sorted, hist, after, h2, act, y, act_shared, total;
-  unsigned ld_logits, max_tiles, max_rows, n_chunks, chunk_ids;
+  size_t ids, rw, logits, sgw, meta, sorted, hist, after, h2, act, y, act_shared, part, total;
+  unsigned ld_logits, max_tiles, max_rows, n_chunks, chunk_ids, router_splits;
 };
+
+// K slices of the router GEMM: its T / 128 x 2 tiles leave most CUs idle
+// at short prompts, each tile a chain of 64 K steps, so up to 8192 tokens
+// the K range is cut into slices whose fp32 partials the top-8 kernel sums
+// (MI355X, whole block: T = 1024 0.420 vs 0.431 ms with 4 slices, 8 and 16
+// no better; T = 2048 0.473 vs 0.481 with 2; T = 8192 0.920 vs 0.925 with 2,
+// 4 slices slower there).
+unsigned router_splits(unsigned T) { return T <= 1024 ? 4u : T <= 8192 ? 2u : 1u; }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
@@ -116,6 +124,9 @@ PfLayout pf_layout(unsigned T, unsigned E) {
   L.act = o;     o = align256(o + (size_t)L.max_rows * kMoeInter * 2);
   L.y = o;       o = align256(o + (size_t)9 * T * kMoeHidden * 2);
   L.act_shared = o;  o = align256(o + (size_t)T * kMoeInter * 2);
+  L.router_splits = router_splits(T);
+  L.part = o;
+  if (L.router_splits > 1) o = align256(o + (size_t)L.router_splits * T * L.ld_logits * 4);
   L.total = o;
   return L;
 }
@@ -157,16 +168,49 @@ __global__ __launch_bounds__(256) void moe_pre_kernel(
 }
 
 // ---- 3. top-8 + routing weights + shared gate, one wave per token ---------
+// With `splits` > 1 the router GEMM left fp32 partials of its K slices
+// (part [splits][T][ld]): the wave sums them in slice order, rounds to bf16
+// and writes the logits row itself.
 __global__ __launch_bounds__(256) void moe_topk_kernel(
-    const bf16* __restrict__ logits, unsigned ld, unsigned E, unsigned T,
-    int* __restrict__ ids_out, float* __restrict__ rw_out, float* __restrict__ sgw) {
+    bf16* __restrict__ logits, const float* __restrict__ part, unsigned splits, unsigned ld,
+    unsigned E, unsigned T, int* __restrict__ ids_out, float* __restrict__ rw_out,
+    float* __restrict__ sgw) {
   const int lane = threadIdx.x & 63;
   const unsigned t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  const bf16* row = logits + (size_t)t * ld;
+  bf16* row = logits + (size_t)t * ld;
   int ids[kMoeTopK];
   float vals[kMoeTopK], rw[kMoeTopK];
-  select_top8(row, E, ids, vals);
+  float sg_logit;
+  if (splits > 1) {
+    // lane l: columns l + 64i, i < 5 (E + 1 <= 257 columns: experts + shared gate)
+    float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    for (unsigned k = 0; k < splits; ++k) {
+      const float* pr = part + ((size_t)k * T + t) * ld;
+#pragma unroll
+      for (int i = 0; i < 5; ++i) {
+        const unsigned e = lane + 64 * i;
+        acc[i] += pr[e <= E ? e : 0u];
+      }
+    }
+    unsigned short raw[4];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const unsigned e = lane + 64 * i;
+      const bf16 b = f2bf(acc[i]);
+      if (e <= E) row[e] = b;
+      if (i < 4) raw[i] = __builtin_bit_cast(unsigned short, b);
+    }
+    select_top8_bits(raw, E, ids, vals);
+    // column E sits in lane E % 64, slot E / 64
+    float v = acc[0];
+#pragma unroll
+    for (int i = 1; i < 5; ++i) v = (int)(E >> 6) == i ? acc[i] : v;
+    sg_logit = bf2f(f2bf(__shfl(v, (int)(E & 63), 64)));
+  } else {
+    select_top8(row, E, ids, vals);
+    sg_logit = bf2f(row[E]);
+  }
   routing_weights(vals, rw);
   if (lane < kMoeTopK) {
     int id = ids[0];
@@ -179,7 +223,7 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
     ids_out[(size_t)t * kMoeTopK + lane] = id;
     rw_out[(size_t)t * kMoeTopK + lane] = w;
   }
-  if (lane == 0) sgw[t] = bf2f(f2bf(1.0f / (1.0f + expf(-bf2f(row[E])))));
+  if (lane == 0) sgw[t] = bf2f(f2bf(1.0f / (1.0f + expf(-sg_logit))));
 }
 
 // ---- 4. slots sorted by group, groups padded to 32 rows, 128-row tiles ----
@@ -371,6 +415,7 @@ struct GemmArgs {
   const float* rw;
   const float* sgw;
   bf16* out;                // logits / act / y
+  float* part;              // router with K slices: fp32 partials [slices][T][ld_out]
   unsigned T, E, ld_out, max_items;
   unsigned shared;          // gate/up, down: the shared expert's T rows in token order
 };
@@ -444,21 +489,25 @@ __device__ __forceinline__ void gemm_k_loop(Fetch& fetch, const char* lds, int a
 // 32wn.., i.e. act columns 32wn..; else 64wn.. and 64wn + 32..).  Fetch
 // instruction i (of (BM + BN) / 8) moves rows 8i..8i+7 of the stage: A rows
 // first, then B rows; wave w issues instructions w * kPfInstr + j.
-template <int MODE>
+// KS > 1 (router only): item i covers K slice i % KS of tile i / KS.
+template <int MODE, int KS = 1>
 __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmArgs p) {
+  static_assert(KS == 1 || MODE == kRouter, "K slices are for the router");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   constexpr int K = MODE == kDown ? kMoeInter : kMoeHidden;
-  constexpr int nsteps = K / kPfBK;
+  constexpr int nsteps = K / kPfBK / KS;
+  static_assert(nsteps * kPfBK * KS == K, "K slices");
   const unsigned nb = n_blocks<MODE>(p.E);
   const unsigned m_tiles = (MODE == kRouter || p.shared) ? (p.T + kPfBM - 1) / kPfBM
                                                           : (unsigned)p.meta[0].x;
-  const unsigned items = m_tiles * nb;
+  const unsigned items = m_tiles * nb * KS;
   const unsigned share = (items + 7) / 8;
   const unsigned xi = blockIdx.x >> 3;
   if (xi >= share) return;
   const unsigned item = (blockIdx.x & 7) * share + xi;
   if (item >= items) return;
-  const unsigned mt = item / nb, nt = item % nb;
+  const unsigned ks = item % KS;
+  const unsigned mt = item / KS / nb, nt = item / KS % nb;
   int group = 0, row0, rows;
   if (MODE == kRouter || p.shared) {
     group = MODE == kRouter ? 0 : (int)p.E;
@@ -539,7 +588,7 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) char*)lds));
   auto fetch = [&](int step) {
     const unsigned sbase = lds0 + (step % kPfStages) * kPfStage;
-    const unsigned kb = (unsigned)step * kPfRowB;
+    const unsigned kb = (ks * nsteps + (unsigned)step) * kPfRowB;
 #pragma unroll
     for (int j = 0; j < kPfInstr; ++j) {
       // a dead instruction is still issued, with an out-of-range offset (no
@@ -593,7 +642,12 @@ __global__ __launch_bounds__(64 * kPfWaves, kPfMinWG) void moe_gemm_kernel(GemmA
     for (int i = 0; i < 16; ++i) {
       const int r = kPfWR * wm + 32 * rb + 8 * (i >> 2) + 4 * kh + (i & 3);
       if (r >= rows) continue;
-      if constexpr (MODE == kRouter) {
+      if constexpr (MODE == kRouter && KS > 1) {
+        const unsigned n = nt * kPfBN + 64 * wn + li;
+        float* o = p.part + ((size_t)ks * p.T + row0 + r) * p.ld_out;
+        if (n <= p.E) o[n] = acc[rb][0][i];
+        if (n + 32 <= p.E) o[n + 32] = acc[rb][1][i];
+      } else if constexpr (MODE == kRouter) {
         const unsigned n = nt * kPfBN + 64 * wn + li;
         bf16* o = p.out + (size_t)(row0 + r) * p.ld_out;
         if (n <= p.E) o[n] = f2bf(acc[rb][0][i]);
@@ -708,6 +762,8 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   static hipError_t attr_status = hipSuccess;
   std::call_once(attr_once, [] {
     for (const void* f : {reinterpret_cast<const void*>(moe_gemm_kernel<kRouter>),
+                          reinterpret_cast<const void*>(moe_gemm_kernel<kRouter, 2>),
+                          reinterpret_cast<const void*>(moe_gemm_kernel<kRouter, 4>),
                           reinterpret_cast<const void*>(moe_gemm_kernel<kGateUp>),
                           reinterpret_cast<const void*>(moe_gemm_kernel<kDown>)}) {
       const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPfLds);
@@ -787,12 +843,16 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
   g.w = win;
   g.out = logits;
   g.ld_out = L.ld_logits;
-  const unsigned router_items = ((T + kPfBM - 1) / kPfBM) * n_blocks<kRouter>(E);
+  g.part = reinterpret_cast<float*>(ws + L.part);
+  const unsigned router_items = ((T + kPfBM - 1) / kPfBM) * n_blocks<kRouter>(E) * L.router_splits;
   g.max_items = router_items;
-  hipLaunchKernelGGL(moe_gemm_kernel<kRouter>, grid_for(router_items), dim3(64 * kPfWaves), kPfLds, st, g);
+  auto router = L.router_splits == 4   ? moe_gemm_kernel<kRouter, 4>
+                : L.router_splits == 2 ? moe_gemm_kernel<kRouter, 2>
+                                       : moe_gemm_kernel<kRouter>;
+  hipLaunchKernelGGL(router, grid_for(router_items), dim3(64 * kPfWaves), kPfLds, st, g);
 
-  hipLaunchKernelGGL(moe_topk_kernel, dim3(tok_blocks), dim3(256), 0, st, logits,
-                     L.ld_logits, E, T, ids, rw, sgw);
+  hipLaunchKernelGGL(moe_topk_kernel, dim3(tok_blocks), dim3(256), 0, st, logits, g.part,
+                     L.router_splits, L.ld_logits, E, T, ids, rw, sgw);
   int* hist = reinterpret_cast<int*>(ws + L.hist);
   hipLaunchKernelGGL(moe_hist_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E, L.n_chunks,
                      L.chunk_ids, hist);

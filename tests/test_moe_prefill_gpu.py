@@ -35,6 +35,7 @@ def _check_routing(ids, rw, logits, n_experts):
     (8, 300, 2),     # 300 rows per expert: five 64-row tiles per group
     (32, 37, 3),     # ragged groups
     (256, 513, 4),   # model geometry, ~16 rows per expert
+    (32, 1500, 5),   # router in two K slices (1024 < T <= 8192)
 ])
 def test_moe_prefill_matches_oracle(gpu, n_experts, tokens, seed):
     from qwen36_attn.moe import MoEBlock
@@ -95,11 +96,18 @@ def test_moe_prefill_8192_tokens_sampled_rows(gpu):
     attn = syn.randn((t, 2048), g, 0.5)
     block = MoEBlock({k: v.to(gpu) for k, v in w.items()})
     print("moe prefill T=8192", flush=True)
-    out, ids, rw, logits, _ = block.prefill(inp.to(gpu), attn.to(gpu), debug=True)
+    out, ids, rw, logits, sg = block.prefill(inp.to(gpu), attn.to(gpu), debug=True)
     torch.cuda.synchronize()
     out, ids, rw, logits = out.cpu(), ids.cpu(), rw.cpu(), logits.cpu().float()
+    sg = sg.cpu().float()
     assert torch.isfinite(out.float()).all()
     rows = torch.randperm(t, generator=syn.gen(621))[:48]
+    # the router's K-sliced partials, summed by the top-8 kernel
+    h2 = O.layer_rmsnorm(inp[rows] + attn[rows], w["post_attention_layernorm"])
+    ref_logits = (h2 @ w["router"].t()).float()
+    assert (logits[rows] - ref_logits).abs().max().item() <= 1e-2 * max(1.0, ref_logits.abs().max().item())
+    ref_sg = (h2 @ w["shared_gate"].t()).float().view(-1)
+    assert (sg[rows] - ref_sg).abs().max().item() <= 1e-2 * max(1.0, ref_sg.abs().max().item())
     _check_routing(ids[rows], rw[rows], logits[rows], 256)
     ref = O.moe_block(inp[rows], attn[rows], w, forced_ids=ids[rows], grouped=True)
     assert (out[rows].float() - ref.float()).abs().max().item() <= TOL
