@@ -269,29 +269,14 @@ __global__ __launch_bounds__(256) void moe_hist_kernel(const int* __restrict__ i
   for (unsigned g = tid; g < E; g += blockDim.x) hist[(size_t)g * n_chunks + blockIdx.x] = cnt[g];
 }
 
-// 4b. one workgroup: group totals, row / tile offsets (one-wave scans), tile
-// table, padding, shared-expert rows, and hist turned into each chunk's
-// first row per group.
-__global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned E, unsigned n_chunks,
-                                                        int* __restrict__ hist,
-                                                        int4* __restrict__ meta,
-                                                        int* __restrict__ sorted) {
-  __shared__ int cnt[kMoeMaxExperts + 1];
-  __shared__ int row_off[kMoeMaxExperts + 2];
-  __shared__ int tile_off[kMoeMaxExperts + 2];
-  const unsigned G = E + 1, tid = threadIdx.x;
-  // totals: 4 threads per group, each summing a quarter of the chunks
-  {
-    const unsigned g = tid >> 2, part = tid & 3;
-    int sum = 0;
-    if (g < E)
-      for (unsigned c = part; c < n_chunks; c += 4) sum += hist[(size_t)g * n_chunks + c];
-    sum += __shfl_xor(sum, 1, 64);
-    sum += __shfl_xor(sum, 2, 64);
-    if (g < E && part == 0) cnt[g] = sum;
-    if (tid == 0) cnt[E] = 0;   // the shared expert runs as launches of its own
-  }
-  __syncthreads();
+// From the group counts cnt[0, G): exclusive offsets of the padded rows and
+// of the tiles (one wave's scans; [G] = totals), the tile table meta and
+// the padding rows of `sorted` (-1).  Called by every thread of the
+// workgroup; ends with the offsets visible to all of them.
+__device__ __forceinline__ void group_offsets(const int* cnt, unsigned G, unsigned tid,
+                                              int* row_off, int* tile_off,
+                                              int4* __restrict__ meta,
+                                              int* __restrict__ sorted) {
   if (tid < 64) {   // one wave: exclusive scans of padded rows and tiles per group
     constexpr int kPer = (kMoeMaxExperts + 1 + 63) / 64;   // 5 groups per lane
     int rows[kPer], tiles[kPer], rsum = 0, tsum = 0;
@@ -333,6 +318,32 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned E, unsigned n_c
       meta[1 + tile_off[g] + j] = int4{(int)g, r0 + kPfBM * j, min(kPfBM, c - kPfBM * j), 0};
     for (int p = r0 + c; p < row_off[g + 1]; ++p) sorted[p] = -1;
   }
+}
+
+// 4b. one workgroup: group totals, row / tile offsets (one-wave scans), tile
+// table, padding, shared-expert rows, and hist turned into each chunk's
+// first row per group.
+__global__ __launch_bounds__(1024) void moe_scan_kernel(unsigned E, unsigned n_chunks,
+                                                        int* __restrict__ hist,
+                                                        int4* __restrict__ meta,
+                                                        int* __restrict__ sorted) {
+  __shared__ int cnt[kMoeMaxExperts + 1];
+  __shared__ int row_off[kMoeMaxExperts + 2];
+  __shared__ int tile_off[kMoeMaxExperts + 2];
+  const unsigned G = E + 1, tid = threadIdx.x;
+  // totals: 4 threads per group, each summing a quarter of the chunks
+  {
+    const unsigned g = tid >> 2, part = tid & 3;
+    int sum = 0;
+    if (g < E)
+      for (unsigned c = part; c < n_chunks; c += 4) sum += hist[(size_t)g * n_chunks + c];
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if (g < E && part == 0) cnt[g] = sum;
+    if (tid == 0) cnt[E] = 0;   // the shared expert runs as launches of its own
+  }
+  __syncthreads();
+  group_offsets(cnt, G, tid, row_off, tile_off, meta, sorted);
   {   // chunk bases: one wave per group, exclusive prefix over the chunks
     const unsigned wave = tid >> 6, lane = tid & 63, waves = blockDim.x / 64;
     if (n_chunks <= 64) {   // every group's counts loaded up front (one round trip)
@@ -401,6 +412,54 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const int* __restrict_
         sorted[atomicAdd(&pos[v[u].z], 1)] = i + 2;
         sorted[atomicAdd(&pos[v[u].w], 1)] = i + 3;
       }
+    }
+  }
+}
+
+// 4'. short prompts (8T <= kAlignOneIds): histogram, offsets and scatter in
+// one workgroup, the ids held in registers (16 per thread) -- one launch
+// instead of 4a-4c.
+constexpr unsigned kAlignOneIds = 16384;
+__global__ __launch_bounds__(1024) void moe_align_one_kernel(const int* __restrict__ ids,
+                                                             unsigned T, unsigned E,
+                                                             int4* __restrict__ meta,
+                                                             int* __restrict__ sorted) {
+  __shared__ int cnt[kMoeMaxExperts + 1];
+  __shared__ int row_off[kMoeMaxExperts + 2];
+  __shared__ int tile_off[kMoeMaxExperts + 2];
+  constexpr int kU = kAlignOneIds / 4 / 1024;
+  const unsigned G = E + 1, tid = threadIdx.x, routed4 = kMoeTopK * T / 4;
+  const int4* ids4 = reinterpret_cast<const int4*>(ids);
+  int4 v[kU];
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const unsigned i = tid + 1024 * u;
+    v[u] = i < routed4 ? ids4[i] : int4{-1, -1, -1, -1};
+  }
+  for (unsigned g = tid; g < G; g += blockDim.x) cnt[g] = 0;   // [E]: shared expert, no rows
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    if (v[u].x >= 0) {
+      atomicAdd(&cnt[v[u].x], 1);
+      atomicAdd(&cnt[v[u].y], 1);
+      atomicAdd(&cnt[v[u].z], 1);
+      atomicAdd(&cnt[v[u].w], 1);
+    }
+  }
+  __syncthreads();
+  group_offsets(cnt, G, tid, row_off, tile_off, meta, sorted);
+  __syncthreads();
+  for (unsigned g = tid; g < G; g += blockDim.x) cnt[g] = row_off[g];   // next row per group
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    if (v[u].x >= 0) {
+      const int i = (int)(4 * (tid + 1024 * u));
+      sorted[atomicAdd(&cnt[v[u].x], 1)] = i;
+      sorted[atomicAdd(&cnt[v[u].y], 1)] = i + 1;
+      sorted[atomicAdd(&cnt[v[u].z], 1)] = i + 2;
+      sorted[atomicAdd(&cnt[v[u].w], 1)] = i + 3;
     }
   }
 }
@@ -853,13 +912,17 @@ Q36_EXPORT int qwen36_moe_prefill(const void* inp, const void* attn_out, const v
 
   hipLaunchKernelGGL(moe_topk_kernel, dim3(tok_blocks), dim3(256), 0, st, logits, g.part,
                      L.router_splits, L.ld_logits, E, T, ids, rw, sgw);
-  int* hist = reinterpret_cast<int*>(ws + L.hist);
-  hipLaunchKernelGGL(moe_hist_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E, L.n_chunks,
-                     L.chunk_ids, hist);
-  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, E, L.n_chunks, hist, meta,
-                     sorted);
-  hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E,
-                     L.n_chunks, L.chunk_ids, hist, sorted);
+  if (kMoeTopK * T <= kAlignOneIds) {
+    hipLaunchKernelGGL(moe_align_one_kernel, dim3(1), dim3(1024), 0, st, ids, T, E, meta, sorted);
+  } else {
+    int* hist = reinterpret_cast<int*>(ws + L.hist);
+    hipLaunchKernelGGL(moe_hist_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E,
+                       L.n_chunks, L.chunk_ids, hist);
+    hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, E, L.n_chunks, hist, meta,
+                       sorted);
+    hipLaunchKernelGGL(moe_scatter_kernel, dim3(L.n_chunks), dim3(256), 0, st, ids, T, E,
+                       L.n_chunks, L.chunk_ids, hist, sorted);
+  }
 
   g.a = h2;
   g.w = static_cast<const bf16*>(expert_gate_up);
