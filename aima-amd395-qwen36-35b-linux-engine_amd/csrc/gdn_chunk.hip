@@ -853,8 +853,11 @@ Q36_EXPORT int qwen36_gdn_chunk_prefill_ex(
   float* so = static_cast<float*>(state_out);
   const bool l2norm = (flags & kFlagQkNormalized) == 0;
   const bool state_vk = (flags & kFlagStateVk) != 0;
-  // Prep over every chunk, then the scan: the scan's workgroups take a whole
-  // CU's LDS, so a concurrent prep would only delay them.
+  // Prep over every chunk, then the scan.  Run side by side (two streams, no
+  // dependency; timing only) they barely overlap: a scan workgroup (93.7 KB
+  // of LDS) cannot join a CU that holds two prep workgroups (2 x 35.8 KB), so
+  // the scan starts as the prep drains (MI355X: T = 8192 0.229 vs 0.230 ms,
+  // 32768 0.892 vs 0.972 ms, 2048 0.075 vs 0.064 ms with the stream fork).
   hipLaunchKernelGGL(gdn_chunk_prep_kernel, dim3(n_chunks, kGdnHv), dim3(256), sizeof(PrepLds), st,
                      qb, kb, qk_heads, qk_token_stride, gb, bb, tokens, wsb, 0u, l2norm);
   hipLaunchKernelGGL(gdn_chunk_scan_kernel, dim3(kGdnHv * kScanGroups), dim3(768),
