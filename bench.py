@@ -44,7 +44,7 @@ def _parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-graph", action="store_true", help="time eager launches")
     p.add_argument("--only", choices=["decode", "prefill", "prefill_8k", "prefill_c3", "gdn", "moe",
-                                      "moe_decode", "gemm", "copy", "launch"], default=None,
+                                      "moe_1k", "moe_decode", "gemm", "copy", "launch"], default=None,
                    help="run one leg only (for counter collection); prints no JSON line")
     return p.parse_args()
 
@@ -854,6 +854,8 @@ def run_only(torch, fa, dev, args):
         r = bench_launch_cost(torch, dev)
     elif args.only == "moe":
         r = [bench_moe_prefill(torch, dev, 8192, args.steps, args.warmup)]
+    elif args.only == "moe_1k":
+        r = [bench_moe_prefill(torch, dev, 1024, args.steps, args.warmup)]
     elif args.only == "moe_decode":
         r = [bench_moe_decode(torch, dev, 40, args.steps, args.warmup, False)]
     else:
