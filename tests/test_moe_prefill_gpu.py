@@ -84,18 +84,24 @@ def test_moe_prefill_rows_match_decode(gpu):
     assert same >= 4
 
 
-def test_moe_prefill_8192_tokens_sampled_rows(gpu):
-    """Bench size (T = 8192, E = 256): every output finite, and 48 sampled
-    rows against the oracle (the block is row-independent, so a subset of
-    rows is an exact check of those rows)."""
+@pytest.mark.parametrize("t", [
+    2048,   # the last length aligned by one workgroup (16384 ids)
+    2049,   # the first aligned by histogram / scan / scatter launches
+    8192,   # bench size
+])
+def test_moe_prefill_sampled_rows(gpu, t):
+    """E = 256 at lengths either side of the alignment forms and at the bench
+    size: every output finite, the router logits of 48 sampled rows against
+    h2 @ router^T, their routing against their own logits, and their outputs
+    against the oracle (the block is row-independent, so a subset of rows is
+    an exact check of those rows)."""
     from qwen36_attn.moe import MoEBlock
     g = syn.gen(620)
     w = syn.moe_weights(g, n_experts=256)
-    t = 8192
     inp = syn.randn((t, 2048), g, 0.5)
     attn = syn.randn((t, 2048), g, 0.5)
     block = MoEBlock({k: v.to(gpu) for k, v in w.items()})
-    print("moe prefill T=8192", flush=True)
+    print(f"moe prefill T={t}", flush=True)
     out, ids, rw, logits, sg = block.prefill(inp.to(gpu), attn.to(gpu), debug=True)
     torch.cuda.synchronize()
     out, ids, rw, logits = out.cpu(), ids.cpu(), rw.cpu(), logits.cpu().float()
