@@ -17,21 +17,27 @@
 //           bf16(sigmoid(bf16(h2 . shared_gate)))
 //   out = bf16(after + bf16(bf16(sum_k y_k) + shared))
 //
-// Launches (T tokens, E experts, G = E + 1 groups: the shared expert is group
-// E, holding every token, so it rides the same grouped GEMMs):
+// Launches (T tokens, E experts; the shared expert's rows are every token
+// in order, so its two GEMMs need no routing and run on a side stream,
+// forked after 1 and joined before 7, beside 2-4):
 //  1. moe_pre_kernel       residual + RMSNorm, one wave per token.
-//  2. moe_gemm<kRouter>    logits [T, E + 1] = h2 [router | shared_gate]^T.
+//  2. moe_gemm<kRouter>    logits [T, E + 1] = h2 [router | shared_gate]^T;
+//                          up to 8192 tokens in K slices whose fp32
+//                          partials 3 sums.
 //  3. moe_topk_kernel      top-8 + routing softmax + shared gate, a wave per token.
-//  4. moe_hist/scan/scatter (token, rank) slots sorted by expert, each group
+//  4. alignment            (token, rank) slots sorted by expert, each group
 //                          padded to 32 rows and cut into tiles of up to 128
-//                          rows: per-chunk histograms, one scan workgroup,
-//                          per-chunk scatter.
+//                          rows: one workgroup up to 2048 tokens
+//                          (moe_align_one), else per-chunk histograms, one
+//                          scan workgroup and a per-chunk scatter.
 //  5. moe_gemm<kGateUp>    act [tile rows, 512] = silu(gate) * up per tile,
-//                          gate and up columns of one group in one workgroup.
+//                          gate and up columns of one group in one workgroup
+//                          (side stream: the shared expert's T rows).
 //  6. moe_gemm<kDown>      y rows scaled by their routing weight, scattered to
-//                          their (token, rank) slot.
-//  7. moe_combine_kernel   per token: sum of the 8 routed rows, + shared, +
-//                          after.
+//                          their (token, rank) slot (side stream: the shared
+//                          rows, unscaled).
+//  7. moe_combine_kernel   per token: sum of the 8 routed rows, + the shared
+//                          row scaled by its gate, + after.
 //
 // Grouped GEMM: a workgroup computes one tile of up to 128 rows of one
 // group against 256 weight rows, K in steps of 32, with 8 waves of 64 x 64 on
