@@ -326,10 +326,10 @@ class LinearAttentionLayer:
             core, _ = recurrent_gated_delta_rule(q, k, v, g, beta, self.ssm_state,
                                                  final_state=self.ssm_state)
         else:
-            new_state = torch.empty_like(self.ssm_state)
+            # in place: each scan lane reads its state elements before it
+            # writes them, so the state keeps its buffer (prefix-cache slices)
             core, _ = chunk_gated_delta_rule(q, k, v, g, beta, self.ssm_state,
-                                             final_state=new_state)
-            self.ssm_state.copy_(new_state)   # keep the state buffer (prefix-cache slices)
+                                             final_state=self.ssm_state)
         gated = gated_rmsnorm(core, z, w["norm"])
         return linear(gated, w["out_proj"])
 

@@ -95,6 +95,22 @@ def test_recurrent_in_place_state_and_repeated_heads(gpu):
     assert (out.cpu().float() - ref_o.float()).abs().max().item() <= TOL_OUT
 
 
+def test_chunk_prefill_in_place_state(gpu):
+    """state_out aliasing state_in (the layer's prefill path): bit-identical
+    to a separate output buffer, with a ragged last chunk."""
+    from qwen36_attn import gated_deltanet as G
+    g = syn.gen(8)
+    q, k, v, gg, beta = [x.to(gpu) for x in syn.gdn_core_inputs(300, g, a_max=1.0)]
+    s0 = torch.randn(32, 128, 128, generator=g).to(gpu)
+    sep = torch.empty_like(s0)
+    out_a, _ = G.chunk_gated_delta_rule(q, k, v, gg, beta, s0, final_state=sep)
+    sd = s0.clone()
+    out_b, _ = G.chunk_gated_delta_rule(q, k, v, gg, beta, sd, final_state=sd)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(sep, sd)
+
+
 def test_config4_prefill_then_decode(gpu):
     """Config 4: chunked prefill of 8192 tokens from zero state, then 64
     recurrent decode steps carrying the fp32 state."""
