@@ -105,11 +105,14 @@ Q36_EXPORT int qwen36_prefill_gemm_bf16_lt(const void* x, unsigned ldx, const vo
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kLtMaxDevices) return Q36_EINVAL;
   // Output widths past a multiple of 4096 run as two products (the first
-  // n1 = 4096-multiple columns, then the rest): the heuristic's algorithm
-  // for the fused widths is far from its best there (MI355X, T = 8192:
-  // N = 12352 443 us vs 12288 + 64 in 285 + 10 us; N = 9216 274 us vs
-  // 8192 + 1024 in 196 + 33 us).
-  const unsigned n1 = (n > 4096u && n % 4096u != 0u) ? n / 4096u * 4096u : n;
+  // n1 = 4096-multiple columns, then the rest) from 513 rows on: the
+  // heuristic's algorithm for the fused widths is far from its best there
+  // (MI355X, T = 8192: N = 12352 443 us vs 12288 + 64 in 285 + 10 us; N =
+  // 9216 274 us vs 8192 + 1024 in 196 + 33 us), while for short prompts the
+  // second launch costs more than it saves (T = 256: N = 9216 22.4 vs 28.5
+  // us, N = 12352 22.6 vs 30.8; T = 512: 26.0 vs 30.6, 33.0 vs 35.9).
+  const unsigned n1 =
+      (m > 512u && n > 4096u && n % 4096u != 0u) ? n / 4096u * 4096u : n;
   const LtPlan* p = lt_plan(dev, m, n1, k, ldx, ldy);
   const LtPlan* p2 = n1 < n ? lt_plan(dev, m, n - n1, k, ldx, ldy) : nullptr;
   if (p == nullptr || (n1 < n && p2 == nullptr))

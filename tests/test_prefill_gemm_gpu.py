@@ -45,15 +45,17 @@ def test_prefill_gemm_strided_operands(gpu, backend):
     assert (yb[:, :500] == 7).all() and (yb[:, 2548:] == 7).all()
 
 
-def test_prefill_gemm_lt_split_width_strided_output(gpu):
+@pytest.mark.parametrize("m", [300, 600])
+def test_prefill_gemm_lt_split_width_strided_output(gpu, m):
     """An output width past a multiple of 4096 (4160 = 4096 + 64), which the
-    hipBLASLt entry runs as two products, written into a column slice of a
-    wider output: both parts land in their columns, the rest untouched."""
+    hipBLASLt entry runs as one product up to 512 rows and as two from 513,
+    written into a column slice of a wider output: every part lands in its
+    columns, the rest untouched."""
     from qwen36_attn.prefill_gemm import linear
     g = torch.Generator(device=gpu).manual_seed(6)
-    x = torch.randn(300, 256, generator=g, device=gpu).to(torch.bfloat16)
+    x = torch.randn(m, 256, generator=g, device=gpu).to(torch.bfloat16)
     w = (torch.randn(4160, 256, generator=g, device=gpu) * 0.05).to(torch.bfloat16)
-    yb = torch.full((300, 4400), 7.0, dtype=torch.bfloat16, device=gpu)
+    yb = torch.full((m, 4400), 7.0, dtype=torch.bfloat16, device=gpu)
     y = linear(x, w, out=yb[:, 120:4280], backend="hipblaslt")
     _check(y, x.float() @ w.float().t())
     assert (yb[:, :120] == 7).all() and (yb[:, 4280:] == 7).all()
