@@ -190,13 +190,14 @@ __global__ __launch_bounds__(256) void moe_topk_kernel(
   float sg_logit;
   if (splits > 1) {
     // lane l: columns l + 64i, i < 5 (E + 1 <= 257 columns: experts + shared gate)
-    float acc[5] = {0.f, 0.f, 0.f, 0.f, 0.f};
+    float acc[5];
     for (unsigned k = 0; k < splits; ++k) {
       const float* pr = part + ((size_t)k * T + t) * ld;
 #pragma unroll
       for (int i = 0; i < 5; ++i) {
         const unsigned e = lane + 64 * i;
-        acc[i] += pr[e <= E ? e : 0u];
+        const float x = pr[e <= E ? e : 0u];
+        acc[i] = k == 0 ? x : acc[i] + x;   // slice 0 as is (keeps a -0 sum)
       }
     }
     unsigned short raw[4];
