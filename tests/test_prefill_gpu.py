@@ -52,11 +52,13 @@ def test_prefill_config3_sampled_rows(gpu):
     assert torch.isfinite(got).all()
 
 
-@pytest.mark.parametrize("t", [256, 1536, 2304, 2560])
+@pytest.mark.parametrize("t", [256, 1536, 2304, 2560, 2561])
 def test_short_prompt_split_plans_sampled_rows(gpu, t):
     """Short square prompts through the split plans the chunk-count table
     picks (T = 256: 2 chunks, 1536: 3, 2304 and 2560: 3 over 9 and 10 query
-    tiles), plain and gated: rows at chunk and tile edges against the oracle."""
+    tiles) and the first unsplit length (2561: 11 tiles, a one-row last
+    tile), plain and gated: rows at chunk and tile edges against the
+    oracle."""
     from qwen36_attn.full_attention import fmha_prefill, fmha_prefill_gated, output_gate
     q, k, v = _inputs(t, t, seed=70 + t)
     g = torch.Generator().manual_seed(71 + t)
