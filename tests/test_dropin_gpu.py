@@ -259,3 +259,40 @@ def test_packed_decode_from_conv_output(gpu):
         assert (out[n].float() - ro[0].float()).abs().max().item() <= TOL
         assert ((fin[idx[n]] - rs[0]).norm() / rs.norm()).item() <= 1e-3
     assert torch.equal(fin[1], pool[1])
+
+
+def test_chunk_prefill_ex_state_vk_in_place(gpu):
+    """qwen36_gdn_chunk_prefill_ex in vLLM's [Hv, dv, dk] state orientation
+    with state_out aliasing state_in: bit-identical to separate state
+    buffers (ragged last chunk, q/k already normalised)."""
+    from qwen36_attn import _lib, gated_deltanet as G
+    from qwen36_attn._tensors import ptr, scratch, stream_handle
+    g = syn.gen(95)
+    t = 200
+    q = torch.randn(t, 16, 128, generator=g)
+    k = torch.randn(t, 16, 128, generator=g)
+    q = (q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16).to(gpu)
+    k = (k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16).to(gpu)
+    v = syn.randn((t, 32, 128), g).to(gpu)
+    beta = torch.sigmoid(torch.randn(t, 32, generator=g)).to(gpu)
+    gg = (-torch.nn.functional.softplus(torch.randn(t, 32, generator=g)) * 0.5).to(gpu)
+    h0 = (torch.randn(32, 128, 128, generator=g) * 0.2).to(gpu)      # [Hv, dv, dk]
+    lib = _lib.load(("qwen36_gdn_chunk_prefill_ex",))
+    ws = scratch("gdn_chunk_test", lib.qwen36_gdn_chunk_prefill_workspace_bytes(t), q.device)
+    flags = G.STATE_VK | G.QK_NORMALIZED
+
+    def run(s_in, s_out):
+        out = torch.empty(t, 32, 128, dtype=torch.bfloat16, device=gpu)
+        _lib.call("qwen36_gdn_chunk_prefill_ex", ptr(q), ptr(k), ptr(v), 16, q.stride(0),
+                  v.stride(0), ptr(gg), ptr(beta), ptr(s_in), ptr(s_out), ptr(out), t, flags,
+                  ptr(ws), ws.numel(), stream_handle(q.device))
+        return out
+
+    print("chunk prefill ex, vk state in place", flush=True)
+    sep = torch.empty_like(h0)
+    out_a = run(h0, sep)
+    sd = h0.clone()
+    out_b = run(sd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(sep, sd)
